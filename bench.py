@@ -1,0 +1,216 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X tensor-ring operator (driver contract: one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: y = TR(G1,G2,G3) x, 1920 -> 2880, modes (8,12,20) ->
+(12,10,24), rank 8, fp16, tokens = 1, seeded N(0, sigma^2) cores (make_cores, seed 0) and
+N(0,1) x (generator seed 0 + T), as the reference harness draws them
+(benchmarks/benchmark.py:107-109). A step is one call of the prepared operator; `value` is
+its HIP-event stream latency in us/call over exactly K back-to-back calls, bracketed by
+synchronizes, with x and the packed cores resident in HBM.
+
+The same line carries the other metric cases (tokens 8/32 at rank 8, 1/32 at rank 16, and
+the bf16 Llama-shaped configs) with the dense GEMM of the same shape (F.linear on the
+materialised weight, timed the same way), the dominant kernel's roofline, the launch floors
+and the CPU baseline (the oracle's port of the reference path, fp32, timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "kernel-task_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "µs/call HIP-event latency, tokens 1/8/32, rank 8/16, vs dense fp16 GEMM"
+H100_PUBLISHED_R8_T1_US = 8.18  # ours-B stream, R8 t1, H100 SXM5
+
+CASES = [  # (label, input modes, output modes, rank, dtype, init, tokens)
+    ("r8", (8, 12, 20), (12, 10, 24), 8, "float16", "per_core", (1, 8, 32)),
+    ("r16", (8, 12, 20), (12, 10, 24), 16, "float16", "per_core", (1, 32)),
+    ("llama_up_r8", (16, 16, 16), (16, 28, 32), 8, "bfloat16", "uniform", (1, 8, 32, 128)),
+    ("llama_down_r16", (16, 28, 32), (16, 16, 16), 16, "bfloat16", "uniform", (1, 32, 256)),
+]
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup, headline):
+    import torch
+
+    from factorized_inference import (TRSpec, dense_forward, make_cores,
+                                      materialize_dense_weight, prepare_optimized,
+                                      tr_forward_reference)
+    from factorized_inference import measure as m
+
+    dtype = getattr(torch, dtype_name)
+    spec = TRSpec(ins, outs, rank)
+    cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init=init)
+    t0 = time.perf_counter()
+    run = prepare_optimized(cores, spec)
+    m.synchronize()
+    prep_ms = (time.perf_counter() - t0) * 1e3
+    weight = materialize_dense_weight(cores, spec)
+    results = []
+    for T in tokens:
+        g = torch.Generator(device="cuda").manual_seed(0 + T)
+        x = torch.randn(T, spec.in_features, generator=g, device="cuda", dtype=dtype)
+        ours = lambda: run(x)  # noqa: E731
+        dense = lambda: dense_forward(x, weight)  # noqa: E731
+        for _ in range(warmup):
+            ours()
+            dense()
+        m.synchronize()
+        is_head = headline and T == 1
+        calls = steps if is_head else min(steps, 100)
+        if is_head:
+            m.synchronize()                      # barrier + synchronize on both sides
+            ours_blocks = m.stream_us(ours, calls, blocks=1)
+            m.synchronize()
+        else:
+            ours_blocks = m.stream_us(ours, calls, blocks=3)
+        ours_us = statistics.median(ours_blocks)
+        dense_us = statistics.median(m.stream_us(dense, min(steps, 100), blocks=3))
+        host_ours = statistics.median(m.host_us(ours, 50))
+        host_dense = statistics.median(m.host_us(dense, 50))
+        submit_us = m.host_submit_us(ours, 200)
+        # correctness after timing, against the fp32 factorized path on the same cores
+        y = run(x).float()
+        ref = tr_forward_reference(x.float(), [c.float() for c in cores], spec)
+        err = (y - ref).abs().max().item()
+        info = run.selected(T)
+        case = {
+            "case": label, "tokens": T, "rank": rank, "dtype": dtype_name,
+            "modes": [list(ins), list(outs)], "variant": info["name"], "grid": info["grid"],
+            "lds_bytes": info["lds_bytes"],
+            "ours_stream_us": ours_us, "dense_stream_us": dense_us,
+            "speedup_vs_dense": dense_us / ours_us,
+            "ours_host_us": host_ours, "dense_host_us": host_dense, "ours_submit_us": submit_us,
+            "flops": info["flops"], "bytes": info["bytes"],
+            "max_abs_err_vs_fp32": err, "max_abs_ref": ref.abs().max().item(),
+            "prepare_ms": prep_ms,
+            **m.roofline(info["flops"], info["bytes"], ours_us, dtype),
+        }
+        log(f"{label} T={T}: ours {ours_us:.2f} us, dense {dense_us:.2f} us, "
+            f"err {err:.2e}, {info['name']}")
+        results.append(case)
+    return results
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The oracle's port of the reference CPU path (fp32, reference order), config 1."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from factorized_inference import TRSpec, make_cores
+    from oracle import ring_oracle
+
+    spec = TRSpec()
+    cores = [c.numpy() for c in make_cores(spec, seed=0)]
+    x = torch.randn(1, spec.in_features, generator=torch.Generator().manual_seed(1)).numpy()
+    out = {}
+    for threads in (1, os.cpu_count() or 1):
+        with threadpool_limits(limits=threads):
+            for _ in range(20):
+                ring_oracle.tr_forward(x, cores)
+            samples = []
+            budget = seconds if threads == 1 else seconds / 3
+            t_end = time.perf_counter() + budget
+            while time.perf_counter() < t_end or len(samples) < 100:
+                t0 = time.perf_counter_ns()
+                y = ring_oracle.tr_forward(x, cores)
+                samples.append((time.perf_counter_ns() - t0) / 1000.0)
+        out[threads] = (statistics.median(samples), len(samples))
+        assert np.isfinite(y).all()
+    one, n1 = out[1]
+    many, nmany = out[max(out)]
+    return {
+        "value": one, "unit": "us/call", "cores": 1, "kind": "port",
+        "sample": (f"config 1 (1920->2880, R8, fp32, T=1, per-core sigma, seed 0): median of "
+                   f"{n1} calls of oracle/ring_oracle.tr_forward (the reference's three "
+                   f"contractions in its order, numpy BLAS) with 1 BLAS thread"),
+        "all_cores_value": many, "all_cores": max(out), "all_cores_calls": nmany,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from factorized_inference import _lib
+    from factorized_inference import measure as m
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+    torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
+    torch.set_num_threads(1)
+    with torch.inference_mode():
+        cases = []
+        for i, (label, ins, outs, rank, dt, init, tokens) in enumerate(CASES):
+            if args.headline_only and i > 0:
+                break
+            cases += measure_case(label, ins, outs, rank, dt, init, tokens, args.steps,
+                                  args.warmup, headline=(i == 0))
+        floors = m.floors(_lib.load())
+    head = cases[0]
+    traffic = None
+    traffic_file = ROOT / "profiles" / "traffic_r8_t1.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+    achieved = head["achieved_GBps"]
+    line = {
+        "metric": METRIC,
+        "value": head["ours_stream_us"],
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ours_stream_us"] / 1000.0,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": head["ours_stream_us"] / H100_PUBLISHED_R8_T1_US,
+        "vs_baseline_ref": "BASELINE.md s1: reference fused kernel (ours-B) stream, R8 t1, H100, 8.18 us",
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "tensor-ring linear 1920->2880, modes (8,12,20)->(12,10,24), "
+                               "rank 8, fp16, tokens 1 (BASELINE configs[1])",
+                   "tokens": 1, "rank": 8, "in_features": 1920, "out_features": 2880},
+        "dense_stream_us": head["dense_stream_us"],
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": m.PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": achieved / m.PEAK_HBM_GBS, "traffic": traffic,
+                     "kernel": head["variant"], "algorithmic_bytes": head["bytes"],
+                     "mfma_frac": head["frac_mfma"]},
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
+        "floors": floors,
+        "cases": cases,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,83 @@
+// Internal declarations shared by the HIP sources of libtrk (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "trk.h"
+
+namespace trk {
+
+constexpr int kMaxVariants = 48;
+constexpr int kMaxChains = 6;
+
+// One contraction order, in chain terms. The cores are re-indexed as chain cores
+//   Fc[r1][f][iF][r2], Sc[r2][s][iS][r3], Lc[r3][l][iL][r1]
+// (r1 = link L-F, r2 = link F-S, r3 = link S-L). A forward order follows the ring
+// (G1 -> G2 -> G3 up to rotation) and keeps every core as it is; a backward order swaps the
+// two ring indices of every core. In the packed buffer each chain owns three sections:
+//   Fk[f][r1][r2][KF]  (iF fastest, zero-padded to KF)    first core, stage-1 operand
+//   Sk[s][r3][K2]      (k = iS*R + r2, zero-padded to K2) second core, stage-2 operand
+//   Lk[iL][l][r1][r3]                                    last core, stage-3 operand
+struct Chain {
+    int order[3];    // F, S, L: core indices
+    int forward;     // 1 if the order follows the ring
+    int nF, nS, nL;  // input modes of F, S, L
+    int oF, oS, oL;  // output modes of F, S, L
+    int R;
+    int KF, K2;      // padded stage-1 and stage-2 contraction lengths
+    int sxF, sxS, sxL;  // element strides of iF, iS, iL in a row of x
+    int syF, syS, syL;  // element strides of f, s, l in a row of y
+    size_t offF, offS, offL;  // byte offsets of Fk, Sk, Lk in the packed buffer
+};
+
+struct Plan;
+struct Variant;
+
+using LaunchFn = int (*)(const Plan &, const Variant &, const void *packed, const void *x,
+                         void *y, int tokens, hipStream_t stream);
+
+struct Variant {
+    int kind;        // trk_kernel_kind
+    int chain;       // index into Plan::chains
+    int tile[5];     // TT, FC, SC, LC, IC (generic: IC = ring-link chunk)
+    int block;       // threads per workgroup
+    int lds_bytes;   // dynamic LDS per workgroup
+    int t_min, t_max;
+    char name[64];
+    LaunchFn launch;
+};
+
+struct Plan {
+    int in_modes[3], out_modes[3], rank, dtype, elem;
+    int in_features, out_features;
+    int nchains;
+    Chain chains[kMaxChains];
+    int nvariants;
+    Variant variants[kMaxVariants];
+    size_t packed_bytes;
+};
+
+// error reporting (trk_api.hip)
+int set_error(int status, const char *fmt, ...);
+int check_hip(hipError_t err, const char *what);
+
+// chain geometry (trk_api.hip)
+void describe_chain(const int in_modes[3], const int out_modes[3], int rank, const int order[3],
+                    Chain *chain);
+
+// kernels and their launchers
+int launch_pack(const Plan &plan, const void *g1, const void *g2, const void *g3, void *packed,
+                hipStream_t stream);                                   // trk_pack.hip
+int generic_configure(const Plan &plan, int chain, Variant *v);       // trk_generic.hip
+int launch_generic(const Plan &plan, const Variant &v, const void *packed, const void *x,
+                   void *y, int tokens, hipStream_t stream);           // trk_generic.hip
+int launch_empty(hipStream_t stream);                                  // trk_generic.hip
+
+// MFMA variants compiled for this plan's shape (trk_mfma.hip): appends to plan->variants
+// and returns how many were added.
+int mfma_register(Plan *plan);
+
+}  // namespace trk

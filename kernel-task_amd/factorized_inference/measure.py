@@ -1,0 +1,96 @@
+"""Timing helpers shared by bench.py and the harness (benchmarks/benchmark.py).
+
+Definitions follow the reference's harness (benchmarks/benchmark.py:138-174) and
+tools/measure_kernels.py:36-103:
+  stream latency   HIP events bracketing a block of back-to-back calls on the current
+                   stream, divided by the block length (not a sum of kernel durations)
+  host latency     wall clock around one call including the trailing synchronize
+  floors           an empty C call, and one empty kernel launch (host and stream time)
+  work             algorithmic flops of the chain order the kernel runs, and compulsory
+                   bytes = element size x (factor parameters + T*in + T*out)
+"""
+from __future__ import annotations
+
+import statistics
+import time
+from typing import Callable
+
+import torch
+
+# MI355X (gfx950) peaks: HBM3E 8 TB/s; dense MFMA fp16/bf16 2.5 PFLOP/s, fp32 157.3 TFLOP/s.
+PEAK_HBM_GBS = 8000.0
+PEAK_TFLOPS = {torch.float16: 2500.0, torch.bfloat16: 2500.0, torch.float32: 157.3}
+
+
+def synchronize() -> None:
+    torch.cuda.synchronize()
+
+
+def stream_us(fn: Callable[[], object], calls: int, blocks: int = 1) -> list[float]:
+    """Per-call stream latency (us) of `blocks` event-bracketed blocks of `calls` calls."""
+    out = []
+    for _ in range(blocks):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        synchronize()
+        start.record()
+        for _ in range(calls):
+            fn()
+        end.record()
+        end.synchronize()
+        out.append(start.elapsed_time(end) * 1000.0 / calls)
+    return out
+
+
+def host_us(fn: Callable[[], object], samples: int) -> list[float]:
+    """Host-synchronized latency (us) of single calls."""
+    out = []
+    for _ in range(samples):
+        synchronize()
+        t0 = time.perf_counter_ns()
+        fn()
+        synchronize()
+        out.append((time.perf_counter_ns() - t0) / 1000.0)
+    return out
+
+
+def host_submit_us(fn: Callable[[], object], calls: int) -> float:
+    """Host time per call without synchronizing (what the host needs to submit one call)."""
+    synchronize()
+    t0 = time.perf_counter_ns()
+    for _ in range(calls):
+        fn()
+    t1 = time.perf_counter_ns()
+    synchronize()
+    return (t1 - t0) / 1000.0 / calls
+
+
+def floors(lib, calls: int = 2000) -> dict:
+    """Host cost of an empty C call and of an empty launch; stream time of empty launches."""
+    from .tr_kernel import current_stream_handle
+
+    dev = torch.cuda.current_device()
+    stream = current_stream_handle(dev)
+    t0 = time.perf_counter_ns()
+    for _ in range(calls):
+        lib.trk_empty_call()
+    empty_call = (time.perf_counter_ns() - t0) / 1000.0 / calls
+    launch = lambda: lib.trk_empty_launch(current_stream_handle(dev))  # noqa: E731
+    for _ in range(50):
+        launch()
+    return {
+        "host_empty_c_call_us": empty_call,
+        "host_empty_launch_us": host_submit_us(launch, calls),
+        "stream_empty_launch_us": statistics.median(stream_us(launch, 200, blocks=5)),
+        "stream_handle": bool(stream is not None),
+    }
+
+
+def roofline(flops: float, nbytes: float, us: float, dtype: torch.dtype) -> dict:
+    seconds = us * 1e-6
+    gbs = nbytes / seconds / 1e9
+    tflops = flops / seconds / 1e12
+    return {
+        "achieved_GBps": gbs, "frac_hbm": gbs / PEAK_HBM_GBS,
+        "achieved_TFLOPs": tflops, "frac_mfma": tflops / PEAK_TFLOPS[dtype],
+    }
