@@ -66,12 +66,15 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
         x = torch.randn(T, spec.in_features, generator=g, device="cuda", dtype=dtype)
         ours = lambda: run(x)  # noqa: E731
         dense = lambda: dense_forward(x, weight)  # noqa: E731
-        for _ in range(warmup):
+        one = m.host_us(ours, 1)[0]              # first call; sizes the loops below
+        warm = max(2, min(warmup, int(0.2e6 / max(one, 1.0))))
+        for _ in range(warm):
             ours()
             dense()
         m.synchronize()
         is_head = headline and T == 1
-        calls = steps if is_head else min(steps, 100)
+        # other cases: at most ~0.3 s of calls per block, so no case runs for minutes
+        calls = steps if is_head else max(5, min(steps, 100, int(0.3e6 / max(one, 1.0))))
         if is_head:
             m.synchronize()                      # barrier + synchronize on both sides
             ours_blocks = m.stream_us(ours, calls, blocks=1)
@@ -80,9 +83,9 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
             ours_blocks = m.stream_us(ours, calls, blocks=3)
         ours_us = statistics.median(ours_blocks)
         dense_us = statistics.median(m.stream_us(dense, min(steps, 100), blocks=3))
-        host_ours = statistics.median(m.host_us(ours, 50))
+        host_ours = statistics.median(m.host_us(ours, min(50, calls)))
         host_dense = statistics.median(m.host_us(dense, 50))
-        submit_us = m.host_submit_us(ours, 200)
+        submit_us = m.host_submit_us(ours, min(200, calls))
         # correctness after timing, against the fp32 factorized path on the same cores
         y = run(x).float()
         ref = tr_forward_reference(x.float(), [c.float() for c in cores], spec)

@@ -62,6 +62,8 @@ typedef struct trk_variant_info {
     int t_max;      /* largest token count the default selection routes here */
     double flops;   /* algorithmic flops of one launch at that token count, no padding */
     double bytes;   /* compulsory HBM bytes of one launch: cores + x + y */
+    size_t packed_offset[3]; /* byte offsets in the packed buffer of the first, second and
+                                last core as this variant's kernel reads them */
 } trk_variant_info;
 
 /* ABI version of the library (TRK_ABI_VERSION it was built with). No reference counterpart;
@@ -110,7 +112,8 @@ int trk_pack(const trk_plan *plan, const void *g1, const void *g2, const void *g
              void *packed, void *stream);
 
 /* y = TR(cores) x for `tokens` rows of x, on `stream`, with the variant the plan selects.
- * x and packed are only read; y is fully written; tokens == 0 launches nothing.
+ * x and packed are only read; y is fully written; tokens == 0 launches nothing. x and packed
+ * must be 16-byte aligned (MFMA variants read them with 16-byte loads; TRK_ERR_INVALID).
  * Replaces forward / forward_v3 / forward_v3t (tr_ring.cu:448-463, :1108-1141, :1156-1192),
  * without their workspace, counters and finish pass: each output is owned by one
  * workgroup, so no cross-workgroup reduction or persistent state exists. */

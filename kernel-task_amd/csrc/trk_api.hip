@@ -29,21 +29,6 @@ double chain_flops_per_token(const Plan &p, const Chain &c) {
     return 2.0 * (s1 + s2 + s3);
 }
 
-// Index of the chain with this order in the plan, adding it (and its packed sections).
-int plan_chain(Plan *p, const int order[3]) {
-    for (int i = 0; i < p->nchains; ++i)
-        if (std::equal(order, order + 3, p->chains[i].order)) return i;
-    if (p->nchains == kMaxChains) return -1;
-    Chain &c = p->chains[p->nchains];
-    describe_chain(p->in_modes, p->out_modes, p->rank, order, &c);
-    const size_t e = size_t(p->elem);
-    c.offF = p->packed_bytes;
-    c.offS = align256(c.offF + e * size_t(c.oF) * c.R * c.R * c.KF);
-    c.offL = align256(c.offS + e * size_t(c.oS) * c.R * c.K2);
-    p->packed_bytes = align256(c.offL + e * size_t(c.nL) * c.oL * c.R * c.R);
-    return p->nchains++;
-}
-
 const Plan *as_plan(const trk_plan *plan) { return reinterpret_cast<const Plan *>(plan); }
 Plan *as_plan(trk_plan *plan) { return reinterpret_cast<Plan *>(plan); }
 
@@ -61,6 +46,21 @@ void grid_of(const Plan &p, const Variant &v, int tokens, int grid[3]) {
     }
 }
 }  // namespace
+
+// Index of the chain with this order in the plan, adding it (and its packed sections).
+int plan_chain(Plan *p, const int order[3]) {
+    for (int i = 0; i < p->nchains; ++i)
+        if (std::equal(order, order + 3, p->chains[i].order)) return i;
+    if (p->nchains == kMaxChains) return -1;
+    Chain &c = p->chains[p->nchains];
+    describe_chain(p->in_modes, p->out_modes, p->rank, order, &c);
+    const size_t e = size_t(p->elem);
+    c.offF = p->packed_bytes;
+    c.offS = align256(c.offF + e * size_t(c.oF) * c.R * c.R * c.KF);
+    c.offL = align256(c.offS + e * size_t(c.oS) * c.R * c.K2);
+    p->packed_bytes = align256(c.offL + e * size_t(c.nL) * c.oL * c.R * c.R);
+    return p->nchains++;
+}
 
 int set_error(int status, const char *fmt, ...) {
     va_list args;
@@ -208,6 +208,9 @@ int trk_plan_describe(const trk_plan *plan, int variant, int tokens, trk_variant
     double params = 0.0;
     for (int m = 0; m < 3; ++m) params += double(p.rank) * p.rank * p.in_modes[m] * p.out_modes[m];
     info->bytes = double(p.elem) * (params + double(tokens) * (p.in_features + p.out_features));
+    info->packed_offset[0] = c.offF;
+    info->packed_offset[1] = c.offS;
+    info->packed_offset[2] = c.offL;
     return TRK_OK;
 }
 
@@ -255,6 +258,9 @@ int trk_forward_variant(const trk_plan *plan, int variant, const void *packed, c
     if (variant < 0 || variant >= p.nvariants)
         return set_error(TRK_ERR_INVALID, "trk_forward: no variant %d", variant);
     const Variant &v = p.variants[variant];
+    if (v.kind == TRK_KERNEL_MFMA &&
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(packed)) & 15))
+        return set_error(TRK_ERR_INVALID, "trk_forward: x and packed must be 16-byte aligned");
     return v.launch(p, v, packed, x, y, tokens, static_cast<hipStream_t>(stream));
 }
 

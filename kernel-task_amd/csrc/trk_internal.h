@@ -67,6 +67,8 @@ int check_hip(hipError_t err, const char *what);
 // chain geometry (trk_api.hip)
 void describe_chain(const int in_modes[3], const int out_modes[3], int rank, const int order[3],
                     Chain *chain);
+// index of the plan's chain with this order, added with its packed sections if new (-1: full)
+int plan_chain(Plan *plan, const int order[3]);
 
 // kernels and their launchers
 int launch_pack(const Plan &plan, const void *g1, const void *g2, const void *g3, void *packed,

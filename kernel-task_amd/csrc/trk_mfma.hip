@@ -1,11 +1,597 @@
-// MFMA (gfx950 matrix core) variants of the fused tensor-ring kernel.
+// MFMA (gfx950 matrix core) variants of the fused tensor-ring kernel, fp16 and bf16.
+//
+// Role of the reference's V3 / V3T / V3G kernels (tr_ring.cu:543-751, :822-1056,
+// csrc/v3g/v3g.cuh:142-431); own design for CDNA4:
+//
+// * Output-stationary workgroups. A workgroup owns a tile of the output: TT tokens x FC
+//   digits f of the first chain core x SC digits s of the second x LC digits l of the last,
+//   and loops over every ring piece (iL, r1) itself. There is no fp32 workspace, no atomic
+//   reduction across workgroups and no last-block finish, so nothing crosses the per-XCD L2
+//   caches and a call leaves no state behind. The price is recomputing stage 1 once per
+//   (s, l) chunk, which the chain order and tile choice keep small.
+// * Any contraction order. The host packs the cores for the chain (F, S, L) the variant
+//   uses (trk_pack.hip); the order is picked per shape to cut the rank^3 stage.
+// * Three MFMA GEMMs per step of IC last-core input digits, operands and results in LDS,
+//   each stored K-contiguous so every fragment is one 16- or 8-byte LDS read:
+//     stage 1  U^T[(f,r1,r2), (iL',t,iS)] = Fs[(f,r1,r2), iF]  . Xs[(iL',t,iS), iF]
+//     stage 2  V^T[(s,r3), (iL',r1,t,f)]  = Ss[(s,r3),(iS,r2)] . Ub[(iL',r1,t,f),(iS,r2)]
+//     stage 3  Y[(t,f,s), l]            += Vb[(t,f,s),(iL',r1,r3)] . Ls[iL'][l][(r1,r3)]
+//   A stage's fp32 accumulator rows run along the next stage's K index, so each lane writes
+//   its 4 results as one 8-byte vector in exactly the layout the next stage reads.
+//   Stage 3 accumulates Y in registers over all steps; with fewer Y tiles than waves, its K
+//   range is split over waves and the partial tiles are summed through LDS at the end.
+// * 16x16x32 MFMAs (16x16x16 for a trailing K of 16), wave64, 4 waves per workgroup.
+//
+// Variants are compiled for the shapes and token ranges of the table at the end; plans for
+// other shapes use the generic kernel (trk_generic.hip).
+#include <algorithm>
+#include <cstdio>
+
 #include "trk_internal.h"
 
 namespace trk {
+namespace {
+
+using f32x4 = float __attribute__((ext_vector_type(4)));
+
+template <int DT>
+struct Ops;
+
+template <>
+struct Ops<TRK_DTYPE_F16> {
+    using E = _Float16;
+    using V8 = _Float16 __attribute__((ext_vector_type(8)));
+    using V4 = _Float16 __attribute__((ext_vector_type(4)));
+    using E4 = V4;
+    __device__ static f32x4 k32(V8 a, V8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    __device__ static f32x4 k16(V4 a, V4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Ops<TRK_DTYPE_BF16> {
+    using E = __bf16;
+    using V8 = __bf16 __attribute__((ext_vector_type(8)));
+    using V4 = short __attribute__((ext_vector_type(4)));  // the K16 bf16 MFMA takes raw bits
+    using E4 = __bf16 __attribute__((ext_vector_type(4)));
+    __device__ static f32x4 k32(V8 a, V8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static f32x4 k16(V4 a, V4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
+};
+
+constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int rup(int a, int b) { return cdiv(a, b) * b; }
+constexpr int pick(int m, int a, int b, int c) { return m == 0 ? a : (m == 1 ? b : c); }
+
+// One compiled variant: dtype, shape, contraction order and workgroup tile.
+struct KCfg {
+    int dt;
+    int F, S, L;     // contraction order (core indices)
+    int i0, i1, i2;  // input modes (i, j, k)
+    int o0, o1, o2;  // output modes (p, q, r)
+    int R;
+    int TT, FC, SC, LC, IC;  // tokens, f / s / l digits per workgroup, iL digits per step
+    int KS3;                 // waves sharing one stage-3 tile (split of its K range)
+    int NACC;                // independent accumulator chains per stage-3 tile and wave
+};
+
+template <KCfg C>
+struct Geo {
+    static constexpr int R = C.R, R2 = R * R;
+    static constexpr int nF = pick(C.F, C.i0, C.i1, C.i2);
+    static constexpr int nS = pick(C.S, C.i0, C.i1, C.i2);
+    static constexpr int nL = pick(C.L, C.i0, C.i1, C.i2);
+    static constexpr int oF = pick(C.F, C.o0, C.o1, C.o2);
+    static constexpr int oS = pick(C.S, C.o0, C.o1, C.o2);
+    static constexpr int oL = pick(C.L, C.o0, C.o1, C.o2);
+    static constexpr int IN = C.i0 * C.i1 * C.i2, OUT = C.o0 * C.o1 * C.o2;
+    static constexpr int SXF = pick(C.F, C.i1 * C.i2, C.i2, 1);
+    static constexpr int SXS = pick(C.S, C.i1 * C.i2, C.i2, 1);
+    static constexpr int SXL = pick(C.L, C.i1 * C.i2, C.i2, 1);
+    static constexpr int SYF = pick(C.F, C.o1 * C.o2, C.o2, 1);
+    static constexpr int SYS = pick(C.S, C.o1 * C.o2, C.o2, 1);
+    static constexpr int SYL = pick(C.L, C.o1 * C.o2, C.o2, 1);
+    static constexpr int KF = rup(nF, 16), K2 = rup(nS * R, 16);
+    static constexpr int TT = C.TT, FC = C.FC, SC = C.SC, LC = C.LC, IC = C.IC, KS3 = C.KS3;
+    static constexpr int NACC = C.NACC;
+    // stage 1: A = Fs [M1][KF], B = Xs [N1P][KF]
+    static constexpr int M1 = FC * R2, M1T = M1 / 16;
+    static constexpr int N1 = IC * TT * nS, N1T = cdiv(N1, 16), N1P = N1T * 16;
+    // stage 2: A = Ss [M2P][K2], B = Ub [N2P][K2]
+    static constexpr int M2 = SC * R, M2T = cdiv(M2, 16), M2P = M2T * 16;
+    static constexpr int N2 = IC * R * TT * FC, N2T = cdiv(N2, 16), N2P = N2T * 16;
+    // stage 3: A = Vb [M3P][K3], B = Ls [IC][LCP][R2]
+    static constexpr int M3 = TT * FC * SC, M3T = cdiv(M3, 16), M3P = M3T * 16;
+    static constexpr int N3T = cdiv(LC, 16), LCP = N3T * 16;
+    static constexpr int K3 = IC * R2;
+    static constexpr int NT3 = M3T * N3T, G3 = 4 / KS3, NYW = cdiv(NT3, G3);
+    static constexpr int NSTEP = cdiv(nL, IC);
+    static constexpr int NFC = cdiv(oF, FC), NSC = cdiv(oS, SC), NLC = cdiv(oL, LC);
+    // LDS layout, in elements
+    static constexpr int oFs = 0, szFs = M1 * KF;
+    static constexpr int oSs = oFs + szFs, szSs = M2P * K2;
+    static constexpr int oLs = oSs + szSs, szLs = IC * LCP * R2;
+    static constexpr int oXs = oLs + szLs, szXs = N1P * KF;
+    static constexpr int oUb = oXs + szXs, szUb = N2P * K2;
+    static constexpr int oVb = oUb + szUb, szVb = M3P * K3;
+    static constexpr int LDS_ELEMS = oVb + szVb;
+    static constexpr int LDS_BYTES = LDS_ELEMS * 2;
+    static constexpr int RED_FLOATS = (KS3 - 1) * G3 * NYW * 256;
+    // x loader. Contiguous iF: VX-element vectors straight into Xs rows. Otherwise: 8-element
+    // vectors of the natural x row, scattered element by element, in batches of XB per thread.
+    static constexpr bool XROW = SXF == 1;
+    static constexpr int vx_fits(int v) {
+        return nF % v == 0 && SXS % v == 0 && SXL % v == 0 && IN % v == 0;
+    }
+    static constexpr int VX = !XROW ? 1 : vx_fits(8) ? 8 : vx_fits(4) ? 4 : vx_fits(2) ? 2 : 1;
+    static constexpr int NXV = IC * TT * nS * (nF / VX);     // vectors per step (contiguous iF)
+    static constexpr int NXB = TT * IN / 8;                   // vectors per step (scatter)
+    static constexpr int XB = 8;
+
+    static_assert(R % 8 == 0, "MFMA variants need a rank that is a multiple of 8");
+    static_assert(KS3 == 1 || KS3 == 2 || KS3 == 4, "KS3 must divide the 4 waves");
+    static_assert(NACC >= 1 && (K3 / 32 / KS3) % NACC == 0, "NACC must divide a wave's K steps");
+    static_assert(FC <= oF && SC <= oS && LC <= oL && IC <= nL && TT >= 1, "tile too large");
+    static_assert(LDS_BYTES <= 160 * 1024, "workgroup tile exceeds the 160 KB of LDS");
+    static_assert(RED_FLOATS * 4 <= szUb * 2, "stage-3 reduction does not fit in Ub");
+    static_assert(nL % IC == 0, "IC must divide the last core's input mode");
+    static_assert(XROW || IN % 8 == 0, "scatter loader reads x rows in 8-element vectors");
+};
+
+constexpr int kThreads = 256;
+
+// Wait for every outstanding global load of this wave.
+__device__ inline void wait_loads() { __builtin_amdgcn_s_waitcnt(0); }
+
+// LDS <- global through VGPRs for NB blocks of BLOCK 16-byte vectors: block b is read from
+// src + b * stride (vectors), its first `valid` vectors from memory and the rest zero.
+// issue() starts every read of the copy; commit(), after wait_loads(), writes the LDS.
+template <int NB, int BLOCK>
+struct RegCopy {
+    static constexpr int TOTAL = NB * BLOCK, PER = cdiv(TOTAL, kThreads);
+    uint4 r[PER];
+    __device__ __forceinline__ void issue(const void *src, size_t stride, int valid) {
+        const uint4 *s = static_cast<const uint4 *>(src);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = threadIdx.x + j * kThreads, b = i / BLOCK, w = i % BLOCK;
+            r[j] = make_uint4(0u, 0u, 0u, 0u);
+            if ((TOTAL % kThreads == 0 || i < TOTAL) && w < valid) r[j] = s[b * stride + w];
+        }
+    }
+    __device__ __forceinline__ void commit(void *dst) const {
+        uint4 *d = static_cast<uint4 *>(dst);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = threadIdx.x + j * kThreads;
+            if (TOTAL % kThreads == 0 || i < TOTAL) d[i] = r[j];
+        }
+    }
+};
+
+template <int BYTES>
+struct VecOf;
+template <>
+struct VecOf<16> { using T = uint4; };
+template <>
+struct VecOf<8> { using T = uint2; };
+template <>
+struct VecOf<4> { using T = unsigned int; };
+template <>
+struct VecOf<2> { using T = unsigned short; };
+
+// One LDS GEMM stage: wave `wave` computes tiles wave, wave+4, ... of
+// D[MT*16][NT*16] = A[.][K] . B[.][K]^T (rows K-contiguous, pitch K) and hands each tile to
+// st(mt, nt, d). Tiles go in groups of GRP: every fragment of a group is read from LDS first,
+// then its MFMAs run back to back, then its results are stored, so LDS latency is paid once
+// per group rather than once per K step.
+template <class O, int MT, int NT, int K, class Store>
+__device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename O::E *B, int wave,
+                                         int lrow, int lgrp, Store &&st) {
+    using V8 = typename O::V8;
+    using V4 = typename O::V4;
+    constexpr int TILES = MT * NT, PER = cdiv(TILES, 4);
+    constexpr int K32 = K / 32, K16 = (K % 32) / 16, FR = K32 + K16;
+    constexpr int GRP = PER < 16 / FR ? PER : (16 / FR > 0 ? 16 / FR : 1);
+#pragma unroll
+    for (int j0 = 0; j0 < PER; j0 += GRP) {
+        V8 a8[GRP][K32 > 0 ? K32 : 1], b8[GRP][K32 > 0 ? K32 : 1];
+        V4 a4[GRP], b4[GRP];
+        f32x4 d[GRP];
+#pragma unroll
+        for (int g = 0; g < GRP; ++g) {
+            const int tile = wave + 4 * (j0 + g);
+            if (j0 + g < PER && (TILES % 4 == 0 || tile < TILES)) {
+                const typename O::E *a = A + ((tile / NT) * 16 + lrow) * K;
+                const typename O::E *b = B + ((tile % NT) * 16 + lrow) * K;
+#pragma unroll
+                for (int k = 0; k < K32; ++k) {
+                    a8[g][k] = *reinterpret_cast<const V8 *>(a + 32 * k + 8 * lgrp);
+                    b8[g][k] = *reinterpret_cast<const V8 *>(b + 32 * k + 8 * lgrp);
+                }
+                if constexpr (K16) {
+                    a4[g] = *reinterpret_cast<const V4 *>(a + K - 16 + 4 * lgrp);
+                    b4[g] = *reinterpret_cast<const V4 *>(b + K - 16 + 4 * lgrp);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GRP; ++g) {
+            const int tile = wave + 4 * (j0 + g);
+            if (j0 + g < PER && (TILES % 4 == 0 || tile < TILES)) {
+                d[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k = 0; k < K32; ++k) d[g] = O::k32(a8[g][k], b8[g][k], d[g]);
+                if constexpr (K16) d[g] = O::k16(a4[g], b4[g], d[g]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GRP; ++g) {
+            const int tile = wave + 4 * (j0 + g);
+            if (j0 + g < PER && (TILES % 4 == 0 || tile < TILES)) st(tile / NT, tile % NT, d[g]);
+        }
+    }
+}
+
+template <KCfg C>
+__global__ void __launch_bounds__(kThreads)
+    ring3_mfma_kernel(const typename Ops<C.dt>::E *__restrict__ x,
+                      const typename Ops<C.dt>::E *__restrict__ Fk,
+                      const typename Ops<C.dt>::E *__restrict__ Sk,
+                      const typename Ops<C.dt>::E *__restrict__ Lk,
+                      typename Ops<C.dt>::E *__restrict__ y, int T) {
+    using G = Geo<C>;
+    using O = Ops<C.dt>;
+    using E = typename O::E;
+    using E4 = typename O::E4;
+    constexpr int R = G::R, R2 = G::R2;
+
+    // One LDS array per buffer: distinct objects let the compiler see that stores to one
+    // buffer never alias reads of another, so it can hoist fragment reads across stores.
+    __shared__ __attribute__((aligned(16))) E Fs[G::szFs];
+    __shared__ __attribute__((aligned(16))) E Ss[G::szSs];
+    __shared__ __attribute__((aligned(16))) E Ls[G::szLs];
+    __shared__ __attribute__((aligned(16))) E Xs[G::szXs];
+    __shared__ __attribute__((aligned(16))) E Ub[G::szUb];
+    __shared__ __attribute__((aligned(16))) E Vb[G::szVb];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lrow = lane & 15, lgrp = lane >> 4;
+
+    int b = blockIdx.x;
+    const int l0 = (b % G::NLC) * G::LC;
+    b /= G::NLC;
+    const int s0 = (b % G::NSC) * G::SC;
+    const int f0 = (b / G::NSC) * G::FC;
+    const int t0 = blockIdx.y * G::TT;
+    const int FCv = min(G::FC, G::oF - f0), SCv = min(G::SC, G::oS - s0);
+    const int LCv = min(G::LC, G::oL - l0);
+
+    // Global -> LDS for one step of IC last-core input digits: the last-core slice and x are
+    // read into registers (issue), then written to Ls and Xs[(iL', t, iS)][iF] (commit).
+    // Every global read of a step is in flight before the first wait.
+    using XV = typename VecOf<2 * G::VX>::T;
+    constexpr int XPER = G::XROW ? cdiv(G::NXV, kThreads) : cdiv(G::NXB, kThreads);
+    constexpr int XREG = G::XROW ? XPER : (XPER < G::XB ? XPER : G::XB);
+    XV xr[G::XROW ? XREG : 1];
+    uint4 xb[G::XROW ? 1 : XREG];
+    auto x_row_load = [&](int v, int iL0) {  // contiguous-iF loader: vector v of the step
+        constexpr int cpr = G::nF / G::VX;
+        const int n = v / cpr, c = v % cpr;
+        const int iS = n % G::nS, t = (n / G::nS) % G::TT, iL = iL0 + n / (G::nS * G::TT);
+        XV r{};
+        if ((G::NXV % kThreads == 0 || v < G::NXV) && t0 + t < T)
+            r = *reinterpret_cast<const XV *>(x + size_t(t0 + t) * G::IN + iS * G::SXS +
+                                              iL * G::SXL + c * G::VX);
+        return r;
+    };
+    auto x_scatter_load = [&](int v) {       // scatter loader: 8 contiguous x elements
+        uint4 r = make_uint4(0u, 0u, 0u, 0u);
+        if (v < G::NXB && t0 + v / (G::IN / 8) < T)
+            r = reinterpret_cast<const uint4 *>(x + size_t(t0) * G::IN)[v];
+        return r;
+    };
+    auto x_scatter_store = [&](int v, uint4 r, int iL0) {
+        const int t = v / (G::IN / 8);
+        if (v >= G::NXB || t0 + t >= T) return;
+        const E *e = reinterpret_cast<const E *>(&r);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int flat = (v % (G::IN / 8)) * 8 + q;
+            const int m0 = flat / (C.i1 * C.i2), m1 = (flat / C.i2) % C.i1, m2 = flat % C.i2;
+            const int iF = pick(C.F, m0, m1, m2), iS = pick(C.S, m0, m1, m2);
+            const int ilp = pick(C.L, m0, m1, m2) - iL0;
+            if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nS + iS) * G::KF + iF] = e[q];
+        }
+    };
+    RegCopy<1, G::szFs / 8> cF;
+    RegCopy<1, G::szSs / 8> cS;
+    RegCopy<G::IC, G::LCP * R2 / 8> cL;
+    auto issue_step = [&](int iL0) {
+        cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
+        if constexpr (G::XROW) {
+#pragma unroll
+            for (int j = 0; j < XREG; ++j) xr[j] = x_row_load(tid + j * kThreads, iL0);
+        } else {
+#pragma unroll
+            for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * kThreads);
+        }
+    };
+    auto commit_step = [&](int iL0) {
+        wait_loads();
+        cL.commit(Ls);
+        if constexpr (G::XROW) {
+            constexpr int cpr = G::nF / G::VX;
+#pragma unroll
+            for (int j = 0; j < XREG; ++j) {
+                const int v = tid + j * kThreads;
+                if ((G::NXV % kThreads == 0 || v < G::NXV) && t0 + (v / cpr / G::nS) % G::TT < T)
+                    *reinterpret_cast<XV *>(Xs + (v / cpr) * G::KF + (v % cpr) * G::VX) = xr[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < XREG; ++j) x_scatter_store(tid + j * kThreads, xb[j], iL0);
+            for (int j0 = XREG; j0 < XPER; j0 += XREG) {  // further batches, one latency each
+#pragma unroll
+                for (int j = 0; j < XREG; ++j)
+                    xb[j] = j0 + j < XPER ? x_scatter_load(tid + (j0 + j) * kThreads)
+                                          : make_uint4(0u, 0u, 0u, 0u);
+                wait_loads();
+#pragma unroll
+                for (int j = 0; j < XREG; ++j)
+                    if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * kThreads, xb[j], iL0);
+            }
+        }
+    };
+
+    // the first- and second-core slices stay resident for the whole call
+    cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
+    cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
+    issue_step(0);
+    // While the loads fly: zero what no load writes (Xs K padding, Xs rows of absent tokens,
+    // Ub K padding).
+    for (int i = tid; i < G::N1P * G::KF; i += kThreads) {
+        const int n = i / G::KF, iF = i % G::KF;
+        if (iF >= G::nF || n >= G::N1 || t0 + (n / G::nS) % G::TT >= T) Xs[i] = E(0.0f);
+    }
+    if constexpr (G::K2 > G::nS * R) {
+        constexpr int pad = G::K2 - G::nS * R;
+        for (int i = tid; i < G::N2P * pad; i += kThreads)
+            Ub[(i / pad) * G::K2 + G::nS * R + i % pad] = E(0.0f);
+    }
+    commit_step(0);
+    cF.commit(Fs);
+    cS.commit(Ss);
+    __syncthreads();
+
+    f32x4 acc[G::NYW][G::NACC];
+#pragma unroll
+    for (int j = 0; j < G::NYW; ++j)
+#pragma unroll
+        for (int c = 0; c < G::NACC; ++c) acc[j][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int g3 = wave / G::KS3, part3 = wave % G::KS3;
+    constexpr int K3STEPS = G::K3 / 32, PERK = K3STEPS / G::KS3;
+    static_assert(K3STEPS % G::KS3 == 0, "stage-3 K steps must split evenly over KS3 waves");
+
+    for (int step = 0; step < G::NSTEP; ++step) {
+        const int iL0 = step * G::IC;
+        if (step > 0) {
+            __syncthreads();  // stage 3 of the previous step is done with Ls and Vb
+            commit_step(iL0);  // its loads were issued at the start of the previous step
+            __syncthreads();
+        }
+        // prefetch the next step's last-core slice and x into registers; they land while
+        // this step computes, so a step pays no memory latency of its own
+        if (step + 1 < G::NSTEP) issue_step(iL0 + G::IC);
+
+        // stage 1: U^T = Fs . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]
+        lds_gemm<O, G::M1T, G::N1T, G::KF>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            const int n = nt * 16 + lrow;
+            if (G::N1 % 16 == 0 || n < G::N1) {
+                const int iS = n % G::nS, t = (n / G::nS) % G::TT, ilp = n / (G::nS * G::TT);
+                const int m0 = mt * 16 + 4 * lgrp;
+                const int r2 = m0 % R, r1 = (m0 / R) % R, f = m0 / R2;
+                E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
+                *reinterpret_cast<E4 *>(Ub + (((ilp * R + r1) * G::TT + t) * G::FC + f) * G::K2 +
+                                        iS * R + r2) = h;
+            }
+        });
+        __syncthreads();
+
+        // stage 2: V^T = Ss . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)]
+        lds_gemm<O, G::M2T, G::N2T, G::K2>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            const int n = nt * 16 + lrow;
+            const int m0 = mt * 16 + 4 * lgrp;
+            if ((G::N2 % 16 == 0 || n < G::N2) && (G::M2 % 16 == 0 || m0 < G::M2)) {
+                const int f = n % G::FC, t = (n / G::FC) % G::TT, r1 = (n / (G::FC * G::TT)) % R;
+                const int ilp = n / (G::FC * G::TT * R);
+                const int s = m0 / R, r3 = m0 % R;
+                E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
+                *reinterpret_cast<E4 *>(Vb + ((t * G::FC + f) * G::SC + s) * G::K3 +
+                                        (ilp * R + r1) * R + r3) = h;
+            }
+        });
+        __syncthreads();
+
+        // stage 3: Y[(t,f,s), l] += Vb . Ls; each wave of a group takes PERK of the K steps,
+        // reading the fragments of QB steps before running their MFMAs
+        constexpr int QB = PERK < 16 ? PERK : 16;
+        static_assert(PERK % QB == 0 && QB % G::NACC == 0, "stage-3 batches must divide evenly");
+#pragma unroll
+        for (int j = 0; j < G::NYW; ++j) {
+            const int tile = g3 + G::G3 * j;
+            if (G::NT3 % G::G3 == 0 || tile < G::NT3) {
+                const int mt = tile / G::N3T, nt = tile % G::N3T;
+                const E *a = Vb + (mt * 16 + lrow) * G::K3;
+                const int l = nt * 16 + lrow;
+#pragma unroll
+                for (int q0 = 0; q0 < PERK; q0 += QB) {
+                    typename O::V8 af[QB], bf[QB];
+#pragma unroll
+                    for (int q = 0; q < QB; ++q) {
+                        const int k = (part3 * PERK + q0 + q) * 32;
+                        af[q] = *reinterpret_cast<const typename O::V8 *>(a + k + 8 * lgrp);
+                        bf[q] = *reinterpret_cast<const typename O::V8 *>(
+                            Ls + ((k / R2) * G::LCP + l) * R2 + k % R2 + 8 * lgrp);
+                    }
+#pragma unroll
+                    for (int q = 0; q < QB; ++q)
+                        acc[j][q % G::NACC] = O::k32(af[q], bf[q], acc[j][q % G::NACC]);
+                }
+            }
+        }
+    }
+
+    // sum the independent chains, then the K-split partials of the waves through LDS
+#pragma unroll
+    for (int j = 0; j < G::NYW; ++j)
+#pragma unroll
+        for (int c = 1; c < G::NACC; ++c) acc[j][0] += acc[j][c];
+    if constexpr (G::KS3 > 1) {
+        __syncthreads();
+        float *red = reinterpret_cast<float *>(Ub);
+        if (part3 > 0) {
+#pragma unroll
+            for (int j = 0; j < G::NYW; ++j)
+                *reinterpret_cast<f32x4 *>(red + (((part3 - 1) * G::G3 + g3) * G::NYW + j) * 256 +
+                                           lane * 4) = acc[j][0];
+        }
+        __syncthreads();
+        if (part3 == 0) {
+#pragma unroll
+            for (int j = 0; j < G::NYW; ++j)
+#pragma unroll
+                for (int p = 1; p < G::KS3; ++p)
+                    acc[j][0] += *reinterpret_cast<const f32x4 *>(
+                        red + (((p - 1) * G::G3 + g3) * G::NYW + j) * 256 + lane * 4);
+        }
+    }
+    if (part3 != 0) return;
+
+    // write y[t, f, s, l] (permuted back to (p, q, r) by the compile-time strides)
+#pragma unroll
+    for (int j = 0; j < G::NYW; ++j) {
+        const int tile = g3 + G::G3 * j;
+        if (tile >= G::NT3) continue;
+        const int mt = tile / G::N3T, nt = tile % G::N3T;
+        const int l = nt * 16 + lrow;
+        if (l >= LCv) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = mt * 16 + 4 * lgrp + i;
+            const int s = m % G::SC, f = (m / G::SC) % G::FC, t = m / (G::SC * G::FC);
+            if (m < G::M3 && s < SCv && f < FCv && t0 + t < T)
+                y[size_t(t0 + t) * G::OUT + (f0 + f) * G::SYF + (s0 + s) * G::SYS +
+                  (l0 + l) * G::SYL] = E(acc[j][0][i]);
+        }
+    }
+}
+
+template <KCfg C>
+int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const void *x, void *y,
+                int tokens, hipStream_t stream) {
+    using G = Geo<C>;
+    using E = typename Ops<C.dt>::E;
+    const Chain &c = plan.chains[v.chain];
+    const char *base = static_cast<const char *>(packed);
+    const dim3 grid(G::NFC * G::NSC * G::NLC, (tokens + G::TT - 1) / G::TT);
+    if (grid.y > 65535u)
+        return set_error(TRK_ERR_UNSUPPORTED, "trk_forward: %d tokens exceed one launch of %s",
+                         tokens, v.name);
+    hipLaunchKernelGGL(ring3_mfma_kernel<C>, grid, dim3(kThreads), 0, stream,
+                       static_cast<const E *>(x), reinterpret_cast<const E *>(base + c.offF),
+                       reinterpret_cast<const E *>(base + c.offS),
+                       reinterpret_cast<const E *>(base + c.offL), static_cast<E *>(y), tokens);
+    return check_hip(hipGetLastError(), "trk_forward: MFMA kernel launch");
+}
+
+struct Entry {
+    KCfg cfg;
+    int t_min, t_max;  // default token range (0, 0: only reachable by index)
+    int lds_bytes;
+    LaunchFn launch;
+};
+
+#define TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC) \
+    KCfg { DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC }
+#define TRK_ENTRY(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, TMIN,   \
+                  TMAX)                                                                          \
+    {TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC), TMIN, TMAX,  \
+     Geo<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3,                \
+                 NACC)>::LDS_BYTES,                                                               \
+     launch_mfma<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC)>},
+
+constexpr int H = TRK_DTYPE_F16, B = TRK_DTYPE_BF16;
+
+// dtype, order F S L, input modes, output modes, rank, tile TT FC SC LC IC, stage-3 KS3 NACC,
+// default token range (0 0: reachable by index only)
+const Entry kEntries[] = {
+    // 1920 -> 2880, (8,12,20) -> (12,10,24), rank 8, fp16
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 1, 4, 1, 1)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 1, 12, 8, 1, 4, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 5, 12, 8, 1, 4, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 2, 1 << 30)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 2, 5, 12, 8, 1, 4, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 4, 1, 10, 12, 4, 2, 1, 0, 0)
+    // same modes, rank 16, fp16
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 2, 2, 1, 1)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 2, 12, 4, 4, 1, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 5, 12, 4, 1, 4, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 2, 1 << 30)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 5, 12, 2, 2, 1, 0, 0)
+    // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 2, 2, 1, 1)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 4, 32, 8, 2, 2, 0, 0)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 7, 32, 8, 1, 2, 0, 0)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 14, 32, 8, 1, 2, 2, 8)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 28, 32, 8, 1, 2, 9, 1 << 30)
+    // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 1, 1)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 2, 16, 2, 4, 1, 0, 0)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 8, 16, 1, 1, 4, 0, 0)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 4, 16, 1, 2, 1, 2, 1 << 30)
+};
+#undef TRK_ENTRY
+#undef TRK_CFG
+
+}  // namespace
 
 int mfma_register(Plan *plan) {
-    (void)plan;
-    return 0;
+    int added = 0;
+    for (const Entry &e : kEntries) {
+        const KCfg &k = e.cfg;
+        const int ins[3] = {k.i0, k.i1, k.i2}, outs[3] = {k.o0, k.o1, k.o2};
+        if (k.dt != plan->dtype || k.R != plan->rank || !std::equal(ins, ins + 3, plan->in_modes) ||
+            !std::equal(outs, outs + 3, plan->out_modes))
+            continue;
+        if (plan->nvariants == kMaxVariants) break;
+        const int order[3] = {k.F, k.S, k.L};
+        const int chain = plan_chain(plan, order);
+        if (chain < 0) continue;
+        Variant &v = plan->variants[plan->nvariants++];
+        v.kind = TRK_KERNEL_MFMA;
+        v.chain = chain;
+        v.tile[0] = k.TT;
+        v.tile[1] = k.FC;
+        v.tile[2] = k.SC;
+        v.tile[3] = k.LC;
+        v.tile[4] = k.IC;
+        v.block = kThreads;
+        v.lds_bytes = e.lds_bytes;
+        v.t_min = e.t_min;
+        v.t_max = e.t_max;
+        v.launch = e.launch;
+        std::snprintf(v.name, sizeof(v.name), "ring3_mfma<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.F,
+                      k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
+        ++added;
+    }
+    return added;
 }
 
 }  // namespace trk

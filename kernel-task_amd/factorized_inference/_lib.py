@@ -37,6 +37,7 @@ class VariantInfo(ctypes.Structure):
         ("t_max", ctypes.c_int),
         ("flops", ctypes.c_double),
         ("bytes", ctypes.c_double),
+        ("packed_offset", ctypes.c_size_t * 3),
     ]
 
     def as_dict(self) -> dict:
@@ -45,6 +46,7 @@ class VariantInfo(ctypes.Structure):
             "order": list(self.order), "tile": list(self.tile), "grid": list(self.grid),
             "block": self.block, "lds_bytes": self.lds_bytes, "t_min": self.t_min,
             "t_max": self.t_max, "flops": self.flops, "bytes": self.bytes,
+            "packed_offset": list(self.packed_offset),
         }
 
 

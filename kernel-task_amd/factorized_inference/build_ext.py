@@ -10,6 +10,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -17,12 +18,16 @@ PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE.parent / "csrc"
 INCLUDE = PACKAGE.parents[1] / "include"
 LIBRARY = PACKAGE / "libtrk.so"
+FASTCALL = PACKAGE / ("_trkcall" + sysconfig.get_config_var("EXT_SUFFIX"))
 OBJ_DIR = PACKAGE.parent / "_build"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no packed fp32 VALU ops (v_pk_*_f32) anywhere in the device code.
+# -amdgpu-kernarg-preload-count: kernel arguments arrive in SGPRs at wave start instead of
+# being fetched from memory first (a memory latency off the front of every launch).
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
@@ -61,6 +66,13 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIBRARY)
+    # the CPython fast-call binding of trk_forward, linked against libtrk.so next to it
+    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-std=c11", f"-I{INCLUDE}",
+           f"-I{sysconfig.get_paths()['include']}", str(CSRC / "trk_pycall.c"),
+           "-o", str(FASTCALL), f"-L{PACKAGE}", "-l:libtrk.so", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
     return LIBRARY
 
 

@@ -26,13 +26,24 @@ _DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16,
            torch.float32: _lib.DTYPE_F32}
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+if _raw_stream is None:
+    _raw_stream = lambda device_index: torch.cuda.current_stream(device_index).cuda_stream  # noqa: E731
+
+
+def _fast_forward():
+    """The CPython fast-call binding of trk_forward (built next to libtrk.so), else ctypes."""
+    _lib.load()  # binds and version-checks libtrk.so first
+    try:
+        from . import _trkcall
+    except ImportError:
+        lib = _lib.load()
+        return lib.trk_forward, lib.trk_forward_variant
+    return _trkcall.forward, _trkcall.forward_variant
 
 
 def current_stream_handle(device_index: int) -> int:
     """hipStream_t of torch's current stream on `device_index`, as an integer."""
-    if _raw_stream is not None:
-        return _raw_stream(device_index)
-    return torch.cuda.current_stream(device_index).cuda_stream
+    return _raw_stream(device_index)
 
 
 class PreparedTRKernel:
@@ -68,8 +79,7 @@ class PreparedTRKernel:
                                             g[2].data_ptr(), self.packed.data_ptr(),
                                             current_stream_handle(self.device_index)))
             del g  # packing is stream-ordered before any later call on this stream
-        self._forward = _lib.load().trk_forward
-        self._forward_variant = _lib.load().trk_forward_variant
+        self._forward, self._forward_variant = _fast_forward()
         self._plan_handle = self.plan.handle
         self._packed_ptr = self.packed.data_ptr()
 
@@ -86,20 +96,23 @@ class PreparedTRKernel:
 
     # ---- calls ---------------------------------------------------------------------------
     def _check(self, x: torch.Tensor) -> torch.Tensor:
-        if x.dtype != self.dtype or x.device != self.device:
+        """x as the kernels read it: same dtype/device, [T, in], contiguous, 16-byte aligned."""
+        if x.dtype is not self.dtype or x.get_device() != self.device_index:
             raise ValueError(f"x must be {self.dtype} on {self.device}, got {x.dtype} on {x.device}")
         if x.ndim != 2 or x.shape[1] != self.in_features:
             raise ValueError(
                 f"Expected x with shape [tokens, {self.in_features}], got {tuple(x.shape)}")
-        return x if x.is_contiguous() else x.contiguous()
+        if not x.is_contiguous() or x.data_ptr() & 15:
+            x = x.clone(memory_format=torch.contiguous_format)
+        return x
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         x = self._check(x)
         tokens = x.shape[0]
-        y = torch.empty((tokens, self.out_features), dtype=self.dtype, device=self.device)
+        y = x.new_empty((tokens, self.out_features))
         if tokens:
             status = self._forward(self._plan_handle, self._packed_ptr, x.data_ptr(),
-                                   y.data_ptr(), tokens, current_stream_handle(self.device_index))
+                                   y.data_ptr(), tokens, _raw_stream(self.device_index))
             if status:
                 _lib.check(status)
         return y
@@ -108,9 +121,9 @@ class PreparedTRKernel:
         """Forward through one explicit variant (tests and sweeps)."""
         x = self._check(x)
         tokens = x.shape[0]
-        y = torch.empty((tokens, self.out_features), dtype=self.dtype, device=self.device)
+        y = x.new_empty((tokens, self.out_features))
         if tokens:
             _lib.check(self._forward_variant(self._plan_handle, int(variant), self._packed_ptr,
                                              x.data_ptr(), y.data_ptr(), tokens,
-                                             current_stream_handle(self.device_index)))
+                                             _raw_stream(self.device_index)))
         return y
