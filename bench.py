@@ -146,6 +146,31 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def traffic_probe(calls: int) -> None:
+    """Workload for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs: `calls` launches of
+    the headline kernel, then a plain 512 MiB device copy (5 launches; larger than every L2
+    and the 256 MB MALL, so its reads come from HBM) whose counters give the scale factor
+    between counted and actual bytes."""
+    import torch
+
+    from factorized_inference import TRSpec, make_cores, prepare_optimized
+
+    spec = TRSpec()
+    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=0)
+    run = prepare_optimized(cores, spec)
+    x = torch.randn(1, spec.in_features, generator=torch.Generator(device="cuda").manual_seed(1),
+                    device="cuda", dtype=torch.float16)
+    for _ in range(calls):
+        run(x)
+    src = torch.ones(256 << 20, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"traffic probe: {calls} x {run.selected(1)['name']}, 5 x copy of "
+          f"{src.numel() * 2} bytes", flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,11 +179,16 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--traffic-probe", type=int, default=0, metavar="CALLS",
+                    help="only run the workload of the HBM-traffic counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         return 2
+    if args.traffic_probe:
+        traffic_probe(args.traffic_probe)
+        return 0
 
     import torch
 

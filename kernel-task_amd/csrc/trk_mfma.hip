@@ -113,6 +113,7 @@ struct Geo {
     static constexpr int NT3 = M3T * N3T, G3 = 4 / KS3, NYW = cdiv(NT3, G3);
     static constexpr int NSTEP = cdiv(nL, IC);
     static constexpr int NFC = cdiv(oF, FC), NSC = cdiv(oS, SC), NLC = cdiv(oL, LC);
+    static constexpr int NBLK = NFC * NSC * NLC;  // workgroups per token tile
     // LDS layout, in elements
     static constexpr int oFs = 0, szFs = M1 * KF;
     static constexpr int oSs = oFs + szFs, szSs = M2P * K2;
@@ -264,7 +265,10 @@ __global__ void __launch_bounds__(kThreads)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lrow = lane & 15, lgrp = lane >> 4;
 
+    // Workgroups are dealt round-robin to the 8 XCDs, each with its own L2. Renumber them so
+    // that consecutive tiles (same first-core digit f, hence the same Fs slice) share an XCD.
     int b = blockIdx.x;
+    if constexpr (G::NBLK % 8 == 0) b = (b % 8) * (G::NBLK / 8) + b / 8;
     const int l0 = (b % G::NLC) * G::LC;
     b /= G::NLC;
     const int s0 = (b % G::NSC) * G::SC;
