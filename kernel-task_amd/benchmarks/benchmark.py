@@ -1,0 +1,297 @@
+"""Isolated per-method benchmark of the tensor-ring operator (the reference harness protocol).
+
+Follows benchmarks/benchmark.py of the reference (78-286): one fresh child process per
+(method, token count); preparation and the first call timed separately; 20 warm-ups; 100
+host-synchronized samples; 5 HIP-event blocks of 20 calls (the headline "stream" latency);
+allocator counters; correctness only after timing, against an fp32 dense oracle built from
+pristine cores; an optional torch.profiler trace at tokens=1. Output: JSON schema 2.
+
+Disclosed changes: `--dtype bfloat16` and `--init uniform` (the benchmark configs' sigma)
+are added; on a CPU device the HIP method is recorded as unavailable instead of running
+(the accelerated path has no CPU fallback).
+
+    python kernel-task_amd/benchmarks/benchmark.py --device cuda --dtype float16 --rank 8 \\
+        --tokens 1,8,32 --output results.json
+"""
+from __future__ import annotations
+
+import argparse
+import gc
+import json
+import platform
+import statistics
+import subprocess
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+import torch
+
+PACKAGE_ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(PACKAGE_ROOT))
+from factorized_inference import (  # noqa: E402
+    TRSpec, dense_forward, make_cores, materialize_dense_weight, prepare_optimized,
+    tr_forward_reference,
+)
+
+METHODS = ("dense", "factorized_reference", "factorized_optimized")
+TOLERANCE = {"float16": 2e-2, "bfloat16": 2e-2, "float32": 1e-4}
+
+
+def triplet(value: str):
+    parts = tuple(int(v) for v in value.split(","))
+    if len(parts) != 3 or min(parts) < 1:
+        raise argparse.ArgumentTypeError("Use three positive integers")
+    return parts
+
+
+def sync(device: torch.device) -> None:
+    if device.type == "cuda":
+        torch.cuda.synchronize(device)
+
+
+def timed(fn, device):
+    sync(device)
+    t0 = time.perf_counter_ns()
+    value = fn()
+    sync(device)
+    return value, (time.perf_counter_ns() - t0) / 1e6
+
+
+def environment(device: torch.device, args) -> dict:
+    smi = None
+    if device.type == "cuda":
+        try:
+            smi = subprocess.check_output(["rocm-smi", "--showproductname"], text=True,
+                                          timeout=10, stderr=subprocess.DEVNULL).strip()
+        except (OSError, subprocess.SubprocessError):
+            smi = "unavailable"
+    return {
+        "python": sys.version, "platform": platform.platform(), "cpu": platform.processor(),
+        "cpu_count": __import__("os").cpu_count(), "torch": torch.__version__,
+        "hip_runtime": getattr(torch.version, "hip", None), "rocm_smi": smi,
+        "device": str(device),
+        "device_name": torch.cuda.get_device_name(device) if device.type == "cuda" else "CPU",
+        "gcn_arch": (torch.cuda.get_device_properties(device).gcnArchName
+                     if device.type == "cuda" else None),
+        "dtype": args.dtype, "init": args.init, "cpu_threads": torch.get_num_threads(),
+    }
+
+
+def errors(actual: torch.Tensor, expected: torch.Tensor) -> dict:
+    diff = (actual.float() - expected.float()).abs()
+    return {
+        "max_absolute_error": diff.max().item(),
+        "mean_absolute_error": diff.mean().item(),
+        "relative_l2_error": (torch.linalg.vector_norm(diff)
+                              / torch.linalg.vector_norm(expected.float()).clamp_min(1e-12)).item(),
+        "max_abs_over_max_ref": diff.max().item() / max(expected.abs().max().item(), 1e-12),
+    }
+
+
+@torch.inference_mode()
+def worker(args) -> dict:
+    device = torch.device(args.device)
+    if device.type == "cuda":
+        torch.cuda.set_device(device)
+    torch.set_num_threads(args.cpu_threads)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+    torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
+    dtype = getattr(torch, args.dtype)
+    spec = TRSpec(args.input_modes, args.output_modes, args.rank)
+    tokens = int(args.tokens)
+    base = {"method": args.worker, "tokens": tokens, "environment": environment(device, args)}
+    if args.worker == "factorized_optimized" and device.type != "cuda":
+        return {**base, "unavailable": "the HIP operator needs a ROCm GPU"}
+
+    probe = torch.empty(1, device=device)
+    del probe
+    sync(device)
+    if device.type == "cuda":
+        torch.cuda.empty_cache()
+        baseline = torch.cuda.memory_allocated(device)
+        torch.cuda.reset_peak_memory_stats(device)
+    cores = make_cores(spec, device=device, dtype=dtype, seed=args.seed, init=args.init)
+    gen = torch.Generator(device=device).manual_seed(args.seed + tokens)
+    x = torch.randn(tokens, spec.in_features, generator=gen, device=device, dtype=dtype)
+    kernel = None
+    if args.worker == "dense":
+        weight, prep_ms = timed(lambda: materialize_dense_weight(cores, spec), device)
+        run = lambda v: dense_forward(v, weight)  # noqa: E731
+        rep_bytes = weight.numel() * weight.element_size()
+        del cores
+    elif args.worker == "factorized_reference":
+        run = lambda v: tr_forward_reference(v, cores, spec)  # noqa: E731
+        prep_ms = 0.0
+        rep_bytes = sum(c.numel() * c.element_size() for c in cores)
+    else:
+        run, prep_ms = timed(lambda: prepare_optimized(cores, spec), device)
+        rep_bytes = sum(c.numel() * c.element_size() for c in cores)
+        info = run.selected(tokens)
+        kernel = {"variant": info["name"], "grid": info["grid"], "lds_bytes": info["lds_bytes"],
+                  "packed_bytes": run.packed_bytes, "flops": info["flops"],
+                  "compulsory_bytes": info["bytes"]}
+
+    first, first_ms = timed(lambda: run(x), device)
+    del first
+    for _ in range(args.warmup):
+        run(x)
+    sync(device)
+    gc.collect()
+    in_bytes = x.numel() * x.element_size()
+    if device.type == "cuda":
+        setup_peak = torch.cuda.max_memory_allocated(device)
+        resident = torch.cuda.memory_allocated(device)
+        torch.cuda.reset_peak_memory_stats(device)
+    samples = []
+    for _ in range(args.iterations):
+        out, ms = timed(lambda: run(x), device)
+        del out
+        samples.append(ms)
+    if device.type == "cuda":
+        peak = torch.cuda.max_memory_allocated(device)
+        memory = {
+            "context_baseline_allocated_bytes": baseline,
+            "input_logical_bytes": in_bytes,
+            "representation_logical_bytes": rep_bytes,
+            "resident_after_warmup_allocated_bytes": resident,
+            "extra_resident_allocated_bytes": max(0, resident - baseline - in_bytes - rep_bytes),
+            "preparation_and_warmup_peak_allocated_bytes": setup_peak,
+            "steady_peak_allocated_bytes": peak,
+            "incremental_workspace_and_output_bytes": peak - resident,
+            "steady_peak_reserved_bytes": torch.cuda.max_memory_reserved(device),
+        }
+    else:
+        memory = {"input_logical_bytes": in_bytes, "representation_logical_bytes": rep_bytes,
+                  "cuda_memory": None}
+    events = []
+    if device.type == "cuda":
+        for _ in range(5):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            sync(device)
+            start.record()
+            for _ in range(args.event_block):
+                run(x)
+            end.record()
+            end.synchronize()
+            events.append(start.elapsed_time(end) / args.event_block)
+
+    # correctness after measurement, against an fp32 dense oracle from pristine cores
+    check = make_cores(spec, device=device, dtype=dtype, seed=args.seed, init=args.init)
+    oracle_w = materialize_dense_weight(tuple(c.float() for c in check), spec)
+    expected = dense_forward(x.float(), oracle_w)
+    actual = run(x)
+    tol = TOLERANCE[args.dtype]
+    torch.testing.assert_close(actual.float(), expected, rtol=tol, atol=tol)
+    correctness = {"rtol": tol, "atol": tol, **errors(actual, expected)}
+    del actual, expected, oracle_w, check
+
+    trace = None
+    if args.profile_dir and tokens == 1:
+        args.profile_dir.mkdir(parents=True, exist_ok=True)
+        trace = args.profile_dir / f"{args.worker}_rank{args.rank}_tokens{tokens}.json"
+        acts = [torch.profiler.ProfilerActivity.CPU]
+        if device.type == "cuda":
+            acts.append(torch.profiler.ProfilerActivity.CUDA)
+        with torch.profiler.profile(activities=acts, record_shapes=True) as prof:
+            for _ in range(3):
+                with torch.profiler.record_function(args.worker):
+                    run(x)
+            sync(device)
+        prof.export_chrome_trace(str(trace))
+
+    return {
+        **base, "preparation_ms": prep_ms, "first_call_ms": first_ms,
+        "host_synchronized_median_ms": statistics.median(samples),
+        "host_synchronized_samples_ms": samples,
+        "cuda_event_stream_median_ms": statistics.median(events) if events else None,
+        "cuda_event_stream_samples_ms": events,
+        "memory": memory, "correctness": correctness, "kernel": kernel,
+        "profiler_trace": str(trace) if trace else None,
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description="Isolated per-method tensor-ring benchmark")
+    ap.add_argument("--device", default="cuda")
+    ap.add_argument("--dtype", choices=tuple(TOLERANCE), default="float16")
+    ap.add_argument("--input-modes", type=triplet, default=TRSpec().input_modes)
+    ap.add_argument("--output-modes", type=triplet, default=TRSpec().output_modes)
+    ap.add_argument("--rank", type=int, default=8)
+    ap.add_argument("--init", choices=("per_core", "uniform"), default="per_core")
+    ap.add_argument("--tokens", default="1,8,32")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--iterations", type=int, default=100)
+    ap.add_argument("--event-block", type=int, default=20)
+    ap.add_argument("--cpu-threads", type=int, default=1)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--output", type=Path, default=Path("benchmark_results.json"))
+    ap.add_argument("--profile-dir", type=Path)
+    ap.add_argument("--worker", choices=METHODS, help=argparse.SUPPRESS)
+    args = ap.parse_args()
+    if min(args.rank, args.warmup, args.iterations, args.event_block, args.cpu_threads) < 1:
+        ap.error("rank, warmup, iterations, event-block and cpu-threads must be positive")
+    if args.device.startswith("cpu") and args.dtype != "float32":
+        ap.error("use float32 on the CPU")
+    try:
+        token_counts = [int(t) for t in args.tokens.split(",")]
+        if not token_counts or min(token_counts) < 1:
+            raise ValueError
+    except ValueError:
+        ap.error("tokens must be comma-separated positive integers")
+    args.output.parent.mkdir(parents=True, exist_ok=True)
+    if args.worker:
+        if len(token_counts) != 1:
+            ap.error("a worker runs exactly one token count")
+        args.output.write_text(json.dumps(worker(args), indent=2) + "\n")
+        return
+
+    spec = TRSpec(args.input_modes, args.output_modes, args.rank)
+    result = {
+        "schema_version": 2,
+        "spec": {"input_modes": spec.input_modes, "output_modes": spec.output_modes,
+                 "rank": spec.rank, "dense_parameters": spec.dense_parameters,
+                 "factor_parameters": spec.factor_parameters},
+        "settings": {k: str(v) if isinstance(v, Path) else v for k, v in vars(args).items()
+                     if k != "worker"},
+        "measurement_notes": [
+            "Each method/token case runs in a fresh child process.",
+            "Host timing includes dispatch and synchronization; HIP events measure block stream time.",
+            "Memory is the PyTorch allocator's; the HIP operator allocates nothing outside it.",
+            "Correctness is checked after measurement against an fp32 dense oracle.",
+        ],
+        "cases": [],
+    }
+    with tempfile.TemporaryDirectory(prefix="tr-benchmark-") as tmp:
+        for tokens in token_counts:
+            case = {"tokens": tokens, "methods": {}}
+            for method in METHODS:
+                out = Path(tmp) / f"{method}-{tokens}.json"
+                cmd = [sys.executable, str(Path(__file__).resolve()), "--worker", method,
+                       "--tokens", str(tokens), "--output", str(out)]
+                for flag in ("device", "dtype", "rank", "init", "warmup", "iterations",
+                             "event_block", "cpu_threads", "seed"):
+                    cmd += ["--" + flag.replace("_", "-"), str(getattr(args, flag))]
+                for flag in ("input_modes", "output_modes"):
+                    cmd += ["--" + flag.replace("_", "-"), ",".join(map(str, getattr(args, flag)))]
+                if args.profile_dir:
+                    cmd += ["--profile-dir", str(args.profile_dir.resolve())]
+                subprocess.run(cmd, check=True)
+                res = json.loads(out.read_text())
+                case["methods"][method] = res
+                if "unavailable" in res:
+                    print(f"tokens={tokens} {method}: {res['unavailable']}", flush=True)
+                    continue
+                ev = res["cuda_event_stream_median_ms"]
+                print(f"tokens={tokens} {method}: host={res['host_synchronized_median_ms']:.4f} ms; "
+                      f"stream={ev if ev is not None else 'N/A'} ms", flush=True)
+            result["cases"].append(case)
+    args.output.write_text(json.dumps(result, indent=2) + "\n")
+    print(f"Wrote {args.output}")
+
+
+if __name__ == "__main__":
+    main()
