@@ -94,6 +94,8 @@ def errors(actual: torch.Tensor, expected: torch.Tensor) -> dict:
 def worker(args) -> dict:
     device = torch.device(args.device)
     if device.type == "cuda":
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
         torch.cuda.set_device(device)
     torch.set_num_threads(args.cpu_threads)
     torch.backends.cuda.matmul.allow_tf32 = False

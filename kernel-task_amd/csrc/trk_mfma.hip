@@ -79,6 +79,7 @@ struct KCfg {
     int TT, FC, SC, LC, IC;  // tokens, f / s / l digits per workgroup, iL digits per step
     int KS3;                 // waves sharing one stage-3 tile (split of its K range)
     int NACC;                // independent accumulator chains per stage-3 tile and wave
+    int WIDE;                // 1: first/second-core slices held in registers, not LDS
 };
 
 template <KCfg C>
@@ -100,6 +101,7 @@ struct Geo {
     static constexpr int KF = rup(nF, 16), K2 = rup(nS * R, 16);
     static constexpr int TT = C.TT, FC = C.FC, SC = C.SC, LC = C.LC, IC = C.IC, KS3 = C.KS3;
     static constexpr int NACC = C.NACC;
+    static constexpr bool WIDE = C.WIDE != 0;
     // stage 1: A = Fs [M1][KF], B = Xs [N1P][KF]
     static constexpr int M1 = FC * R2, M1T = M1 / 16;
     static constexpr int N1 = IC * TT * nS, N1T = cdiv(N1, 16), N1P = N1T * 16;
@@ -115,8 +117,10 @@ struct Geo {
     static constexpr int NFC = cdiv(oF, FC), NSC = cdiv(oS, SC), NLC = cdiv(oL, LC);
     static constexpr int NBLK = NFC * NSC * NLC;  // workgroups per token tile
     // LDS layout, in elements
-    static constexpr int oFs = 0, szFs = M1 * KF;
-    static constexpr int oSs = oFs + szFs, szSs = M2P * K2;
+    static constexpr int oFs = 0, szFs = WIDE ? 8 : M1 * KF;
+    static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * K2;
+    // WIDE: each wave holds the A fragments of BM1 stage-1 and BM2 stage-2 row tiles
+    static constexpr int BM1 = cdiv(M1T, 4), BM2 = cdiv(M2T, 4);
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * R2;
     static constexpr int oXs = oLs + szLs, szXs = N1P * KF;
     static constexpr int oUb = oXs + szXs, szUb = N2P * K2;
@@ -187,56 +191,151 @@ struct VecOf<4> { using T = unsigned int; };
 template <>
 struct VecOf<2> { using T = unsigned short; };
 
-// One LDS GEMM stage: wave `wave` computes tiles wave, wave+4, ... of
-// D[MT*16][NT*16] = A[.][K] . B[.][K]^T (rows K-contiguous, pitch K) and hands each tile to
-// st(mt, nt, d). Tiles go in groups of GRP: every fragment of a group is read from LDS first,
-// then its MFMAs run back to back, then its results are stored, so LDS latency is paid once
-// per group rather than once per K step.
+// Register blocking of one LDS GEMM stage with MT x NT output tiles of 16x16 and KS K
+// steps: blocks of BM x BN tiles go round-robin to the 4 waves; per K step a wave reads BM
+// A fragments and BN B fragments from LDS and runs BM*BN MFMAs on them. The choice weighs
+// a wave's MFMA issue time against its LDS fragment traffic, with at most 16 accumulator
+// tiles per wave.
+struct Blocking {
+    int bm, bn;
+};
+constexpr Blocking choose_blocking(int MT, int NT, int KS) {
+    Blocking best{1, 1};
+    long best_cost = -1;
+    for (int bm = 1; bm <= 4; ++bm)
+        for (int bn = 1; bn <= 8; ++bn) {
+            if (bm * bn > 16 || bm > MT || bn > NT) continue;
+            const int blocks = cdiv(MT, bm) * cdiv(NT, bn);
+            const long per_wave = cdiv(blocks, 4);
+            const long cost = per_wave * KS * (16L * bm * bn + 12L * (bm + bn)) + per_wave * 40;
+            if (best_cost < 0 || cost < best_cost) {
+                best_cost = cost;
+                best = Blocking{bm, bn};
+            }
+        }
+    return best;
+}
+
+// One LDS GEMM stage: D[MT*16][NT*16] = A[.][K] . B[.][K]^T (rows K-contiguous, pitch K),
+// register-blocked as above; each finished tile goes to st(mt, nt, d).
 template <class O, int MT, int NT, int K, class Store>
 __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename O::E *B, int wave,
                                          int lrow, int lgrp, Store &&st) {
     using V8 = typename O::V8;
     using V4 = typename O::V4;
-    constexpr int TILES = MT * NT, PER = cdiv(TILES, 4);
-    constexpr int K32 = K / 32, K16 = (K % 32) / 16, FR = K32 + K16;
-    constexpr int GRP = PER < 16 / FR ? PER : (16 / FR > 0 ? 16 / FR : 1);
+    constexpr int K32 = K / 32, K16 = (K % 32) / 16;
+    constexpr Blocking BK = choose_blocking(MT, NT, K32 + K16);
+    constexpr int BM = BK.bm, BN = BK.bn, NBM = cdiv(MT, BM), NBN = cdiv(NT, BN);
+    constexpr int BLOCKS = NBM * NBN;
 #pragma unroll
-    for (int j0 = 0; j0 < PER; j0 += GRP) {
-        V8 a8[GRP][K32 > 0 ? K32 : 1], b8[GRP][K32 > 0 ? K32 : 1];
-        V4 a4[GRP], b4[GRP];
-        f32x4 d[GRP];
+    for (int j = 0; j < cdiv(BLOCKS, 4); ++j) {
+        const int blk = wave + 4 * j;
+        if (BLOCKS % 4 != 0 && blk >= BLOCKS) break;
+        const int m0 = (blk / NBN) * BM, n0 = (blk % NBN) * BN;
+        const typename O::E *a = A + (m0 * 16 + lrow) * K;
+        const typename O::E *b = B + (n0 * 16 + lrow) * K;
+        f32x4 d[BM][BN];
 #pragma unroll
-        for (int g = 0; g < GRP; ++g) {
-            const int tile = wave + 4 * (j0 + g);
-            if (j0 + g < PER && (TILES % 4 == 0 || tile < TILES)) {
-                const typename O::E *a = A + ((tile / NT) * 16 + lrow) * K;
-                const typename O::E *b = B + ((tile % NT) * 16 + lrow) * K;
+        for (int i = 0; i < BM; ++i)
 #pragma unroll
-                for (int k = 0; k < K32; ++k) {
-                    a8[g][k] = *reinterpret_cast<const V8 *>(a + 32 * k + 8 * lgrp);
-                    b8[g][k] = *reinterpret_cast<const V8 *>(b + 32 * k + 8 * lgrp);
-                }
-                if constexpr (K16) {
-                    a4[g] = *reinterpret_cast<const V4 *>(a + K - 16 + 4 * lgrp);
-                    b4[g] = *reinterpret_cast<const V4 *>(b + K - 16 + 4 * lgrp);
-                }
-            }
+            for (int q = 0; q < BN; ++q) d[i][q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < K32; ++k) {
+            V8 af[BM], bf[BN];
+#pragma unroll
+            for (int i = 0; i < BM; ++i)
+                af[i] = (MT % BM == 0 || m0 + i < MT)
+                            ? *reinterpret_cast<const V8 *>(a + i * 16 * K + 32 * k + 8 * lgrp)
+                            : V8{};
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                bf[q] = (NT % BN == 0 || n0 + q < NT)
+                            ? *reinterpret_cast<const V8 *>(b + q * 16 * K + 32 * k + 8 * lgrp)
+                            : V8{};
+#pragma unroll
+            for (int i = 0; i < BM; ++i)
+#pragma unroll
+                for (int q = 0; q < BN; ++q) d[i][q] = O::k32(af[i], bf[q], d[i][q]);
+        }
+        if constexpr (K16) {
+            V4 af[BM], bf[BN];
+#pragma unroll
+            for (int i = 0; i < BM; ++i)
+                af[i] = (MT % BM == 0 || m0 + i < MT)
+                            ? *reinterpret_cast<const V4 *>(a + i * 16 * K + K - 16 + 4 * lgrp)
+                            : V4{};
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                bf[q] = (NT % BN == 0 || n0 + q < NT)
+                            ? *reinterpret_cast<const V4 *>(b + q * 16 * K + K - 16 + 4 * lgrp)
+                            : V4{};
+#pragma unroll
+            for (int i = 0; i < BM; ++i)
+#pragma unroll
+                for (int q = 0; q < BN; ++q) d[i][q] = O::k16(af[i], bf[q], d[i][q]);
         }
 #pragma unroll
-        for (int g = 0; g < GRP; ++g) {
-            const int tile = wave + 4 * (j0 + g);
-            if (j0 + g < PER && (TILES % 4 == 0 || tile < TILES)) {
-                d[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < BM; ++i)
 #pragma unroll
-                for (int k = 0; k < K32; ++k) d[g] = O::k32(a8[g][k], b8[g][k], d[g]);
-                if constexpr (K16) d[g] = O::k16(a4[g], b4[g], d[g]);
-            }
-        }
+            for (int q = 0; q < BN; ++q)
+                if ((MT % BM == 0 || m0 + i < MT) && (NT % BN == 0 || n0 + q < NT))
+                    st(m0 + i, n0 + q, d[i][q]);
+    }
+}
+
+// A operand held in registers: the fragments of BMW 16-row tiles (rows row0 + i*16 + lane
+// row) over a K range of K, read once from a K-contiguous global matrix (rows at or past
+// `rows` read as zero). Used by the WIDE variants for the first- and second-core slices.
+template <class O, int BMW, int K>
+struct RegA {
+    static constexpr int K32 = K / 32, K16 = (K % 32) / 16;
+    typename O::V8 a8[BMW][K32 > 0 ? K32 : 1];
+    typename O::V4 a4[BMW];
+    __device__ __forceinline__ void load(const typename O::E *__restrict__ src, int row0, int rows,
+                                         int lrow, int lgrp) {
 #pragma unroll
-        for (int g = 0; g < GRP; ++g) {
-            const int tile = wave + 4 * (j0 + g);
-            if (j0 + g < PER && (TILES % 4 == 0 || tile < TILES)) st(tile / NT, tile % NT, d[g]);
+        for (int i = 0; i < BMW; ++i) {
+            const int row = row0 + i * 16 + lrow;
+            const typename O::E *p = src + size_t(row) * K;
+#pragma unroll
+            for (int k = 0; k < K32; ++k)
+                a8[i][k] = row < rows ? *reinterpret_cast<const typename O::V8 *>(p + 32 * k + 8 * lgrp)
+                                      : typename O::V8{};
+            if constexpr (K16)
+                a4[i] = row < rows ? *reinterpret_cast<const typename O::V4 *>(p + K - 16 + 4 * lgrp)
+                                   : typename O::V4{};
         }
+    }
+};
+
+// One LDS GEMM stage with the A operand in registers (RegA, this wave's BMW row tiles): for
+// every column tile nt the wave reads the B fragments once from LDS and runs BMW MFMAs per K
+// step on them, then hands the BMW result tiles to st(nt, d).
+template <class O, int BMW, int K, int NT, class Store>
+__device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typename O::E *B,
+                                         int lrow, int lgrp, Store &&st) {
+    using V8 = typename O::V8;
+    using V4 = typename O::V4;
+    constexpr int K32 = K / 32, K16 = (K % 32) / 16;
+#pragma unroll 2
+    for (int nt = 0; nt < NT; ++nt) {
+        const typename O::E *b = B + (nt * 16 + lrow) * K;
+        V8 b8[K32 > 0 ? K32 : 1];
+        V4 b4{};
+#pragma unroll
+        for (int k = 0; k < K32; ++k) b8[k] = *reinterpret_cast<const V8 *>(b + 32 * k + 8 * lgrp);
+        if constexpr (K16) b4 = *reinterpret_cast<const V4 *>(b + K - 16 + 4 * lgrp);
+        f32x4 d[BMW];
+#pragma unroll
+        for (int i = 0; i < BMW; ++i) d[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < K32; ++k)
+#pragma unroll
+            for (int i = 0; i < BMW; ++i) d[i] = O::k32(A.a8[i][k], b8[k], d[i]);
+        if constexpr (K16)
+#pragma unroll
+            for (int i = 0; i < BMW; ++i) d[i] = O::k16(A.a4[i], b4, d[i]);
+        st(nt, d);
     }
 }
 
@@ -314,8 +413,8 @@ __global__ void __launch_bounds__(kThreads)
             if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nS + iS) * G::KF + iF] = e[q];
         }
     };
-    RegCopy<1, G::szFs / 8> cF;
-    RegCopy<1, G::szSs / 8> cS;
+    RegCopy<1, G::WIDE ? 1 : G::szFs / 8> cF;
+    RegCopy<1, G::WIDE ? 1 : G::szSs / 8> cS;
     RegCopy<G::IC, G::LCP * R2 / 8> cL;
     auto issue_step = [&](int iL0) {
         cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
@@ -355,8 +454,15 @@ __global__ void __launch_bounds__(kThreads)
     };
 
     // the first- and second-core slices stay resident for the whole call
-    cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
-    cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
+    RegA<O, G::BM1, G::KF> fa;
+    RegA<O, G::BM2, G::K2> sa;
+    if constexpr (G::WIDE) {
+        fa.load(Fk + size_t(f0) * R2 * G::KF, wave * G::BM1 * 16, FCv * R2, lrow, lgrp);
+        sa.load(Sk + size_t(s0) * R * G::K2, wave * G::BM2 * 16, SCv * R, lrow, lgrp);
+    } else {
+        cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
+        cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
+    }
     issue_step(0);
     // While the loads fly: zero what no load writes (Xs K padding, Xs rows of absent tokens,
     // Ub K padding).
@@ -370,8 +476,10 @@ __global__ void __launch_bounds__(kThreads)
             Ub[(i / pad) * G::K2 + G::nS * R + i % pad] = E(0.0f);
     }
     commit_step(0);
-    cF.commit(Fs);
-    cS.commit(Ss);
+    if constexpr (!G::WIDE) {
+        cF.commit(Fs);
+        cS.commit(Ss);
+    }
     __syncthreads();
 
     f32x4 acc[G::NYW][G::NACC];
@@ -394,33 +502,65 @@ __global__ void __launch_bounds__(kThreads)
         // this step computes, so a step pays no memory latency of its own
         if (step + 1 < G::NSTEP) issue_step(iL0 + G::IC);
 
-        // stage 1: U^T = Fs . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]
-        lds_gemm<O, G::M1T, G::N1T, G::KF>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
-            const int n = nt * 16 + lrow;
-            if (G::N1 % 16 == 0 || n < G::N1) {
-                const int iS = n % G::nS, t = (n / G::nS) % G::TT, ilp = n / (G::nS * G::TT);
-                const int m0 = mt * 16 + 4 * lgrp;
-                const int r2 = m0 % R, r1 = (m0 / R) % R, f = m0 / R2;
-                E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
-                *reinterpret_cast<E4 *>(Ub + (((ilp * R + r1) * G::TT + t) * G::FC + f) * G::K2 +
-                                        iS * R + r2) = h;
-            }
-        });
+        // stage 1: U^T = F . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]. The Ub offset of an entry is
+        // a row part (r1, f, r2) plus a column part (iL', t, iS).
+        auto ub_row = [&](int m0) {
+            return ((m0 / R) % R * G::TT * G::FC + m0 / R2) * G::K2 + m0 % R;
+        };
+        auto ub_col = [&](int n) {
+            const int iS = n % G::nS, t = (n / G::nS) % G::TT, ilp = n / (G::nS * G::TT);
+            return (ilp * R * G::TT * G::FC + t * G::FC) * G::K2 + iS * R;
+        };
+        auto put4 = [&](E *dst, f32x4 d) {
+            E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
+            *reinterpret_cast<E4 *>(dst) = h;
+        };
+        if constexpr (G::WIDE) {
+            reg_gemm<O, G::BM1, G::KF, G::N1T>(fa, Xs, lrow, lgrp, [&](int nt, const f32x4 *d) {
+                const int n = nt * 16 + lrow;
+                if (G::N1 % 16 != 0 && n >= G::N1) return;
+                const int col = ub_col(n);
+#pragma unroll
+                for (int i = 0; i < G::BM1; ++i) {
+                    const int mt = wave * G::BM1 + i;
+                    if (G::M1T % 4 == 0 || mt < G::M1T) put4(Ub + col + ub_row(mt * 16 + 4 * lgrp), d[i]);
+                }
+            });
+        } else {
+            lds_gemm<O, G::M1T, G::N1T, G::KF>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+                const int n = nt * 16 + lrow;
+                if (G::N1 % 16 == 0 || n < G::N1) put4(Ub + ub_col(n) + ub_row(mt * 16 + 4 * lgrp), d);
+            });
+        }
         __syncthreads();
 
-        // stage 2: V^T = Ss . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)]
-        lds_gemm<O, G::M2T, G::N2T, G::K2>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
-            const int n = nt * 16 + lrow;
-            const int m0 = mt * 16 + 4 * lgrp;
-            if ((G::N2 % 16 == 0 || n < G::N2) && (G::M2 % 16 == 0 || m0 < G::M2)) {
-                const int f = n % G::FC, t = (n / G::FC) % G::TT, r1 = (n / (G::FC * G::TT)) % R;
-                const int ilp = n / (G::FC * G::TT * R);
-                const int s = m0 / R, r3 = m0 % R;
-                E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
-                *reinterpret_cast<E4 *>(Vb + ((t * G::FC + f) * G::SC + s) * G::K3 +
-                                        (ilp * R + r1) * R + r3) = h;
-            }
-        });
+        // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)]: row part (s, r3), column part
+        // (iL', r1, t, f)
+        auto vb_row = [&](int m0) { return (m0 / R) * G::K3 + m0 % R; };
+        auto vb_col = [&](int n) {
+            const int f = n % G::FC, t = (n / G::FC) % G::TT, r1 = (n / (G::FC * G::TT)) % R;
+            const int ilp = n / (G::FC * G::TT * R);
+            return (t * G::FC + f) * G::SC * G::K3 + (ilp * R + r1) * R;
+        };
+        if constexpr (G::WIDE) {
+            reg_gemm<O, G::BM2, G::K2, G::N2T>(sa, Ub, lrow, lgrp, [&](int nt, const f32x4 *d) {
+                const int n = nt * 16 + lrow;
+                if (G::N2 % 16 != 0 && n >= G::N2) return;
+                const int col = vb_col(n);
+#pragma unroll
+                for (int i = 0; i < G::BM2; ++i) {
+                    const int m0 = (wave * G::BM2 + i) * 16 + 4 * lgrp;
+                    if (G::M2 % 64 == 0 || m0 < G::M2) put4(Vb + col + vb_row(m0), d[i]);
+                }
+            });
+        } else {
+            lds_gemm<O, G::M2T, G::N2T, G::K2>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+                const int n = nt * 16 + lrow;
+                const int m0 = mt * 16 + 4 * lgrp;
+                if ((G::N2 % 16 == 0 || n < G::N2) && (G::M2 % 16 == 0 || m0 < G::M2))
+                    put4(Vb + vb_col(n) + vb_row(m0), d);
+            });
+        }
         __syncthreads();
 
         // stage 3: Y[(t,f,s), l] += Vb . Ls; each wave of a group takes PERK of the K steps,
@@ -522,44 +662,55 @@ struct Entry {
     LaunchFn launch;
 };
 
-#define TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC) \
-    KCfg { DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC }
-#define TRK_ENTRY(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, TMIN,   \
-                  TMAX)                                                                          \
-    {TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC), TMIN, TMAX,  \
-     Geo<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3,                \
-                 NACC)>::LDS_BYTES,                                                               \
-     launch_mfma<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC)>},
+#define TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W) \
+    KCfg { DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W }
+#define TRK_ENTRY(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W,      \
+                  TMIN, TMAX)                                                                    \
+    {TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W), TMIN,     \
+     TMAX,                                                                                       \
+     Geo<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC,          \
+                 W)>::LDS_BYTES,                                                                  \
+     launch_mfma<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC,   \
+                         W)>},
 
 constexpr int H = TRK_DTYPE_F16, B = TRK_DTYPE_BF16;
 
 // dtype, order F S L, input modes, output modes, rank, tile TT FC SC LC IC, stage-3 KS3 NACC,
-// default token range (0 0: reachable by index only)
+// WIDE, default token range (0 0: reachable by index only)
 const Entry kEntries[] = {
     // 1920 -> 2880, (8,12,20) -> (12,10,24), rank 8, fp16
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 1, 4, 1, 1)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 1, 12, 8, 1, 4, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 5, 12, 8, 1, 4, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 2, 1 << 30)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 2, 5, 12, 8, 1, 4, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 4, 1, 10, 12, 4, 2, 1, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 1, 4, 0, 1, 1)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 1, 12, 8, 1, 4, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 5, 12, 8, 1, 4, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 2, 5, 12, 8, 1, 4, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 4, 1, 10, 12, 4, 2, 1, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 1, 2, 1 << 30)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 4, 1, 10, 12, 4, 2, 1, 1, 0, 0)
     // same modes, rank 16, fp16
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 2, 2, 1, 1)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 2, 12, 4, 4, 1, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 5, 12, 4, 1, 4, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 2, 1 << 30)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 5, 12, 2, 2, 1, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 2, 2, 0, 1, 1)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 2, 12, 4, 4, 1, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 5, 12, 4, 1, 4, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 5, 12, 2, 2, 1, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 1, 2, 1 << 30)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 10, 12, 2, 2, 1, 1, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 2, 1, 10, 12, 4, 1, 4, 1, 0, 0)
     // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 2, 2, 1, 1)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 4, 32, 8, 2, 2, 0, 0)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 7, 32, 8, 1, 2, 0, 0)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 14, 32, 8, 1, 2, 2, 8)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 28, 32, 8, 1, 2, 9, 1 << 30)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 2, 2, 0, 1, 1)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 4, 32, 8, 2, 2, 0, 0, 0)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 7, 32, 8, 1, 2, 0, 0, 0)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 14, 32, 8, 1, 2, 0, 2, 8)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 28, 32, 8, 1, 2, 0, 9, 64)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 28, 32, 8, 1, 2, 1, 0, 0)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 4, 1, 28, 32, 4, 1, 2, 1, 65, 1 << 30)
     // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 1, 1)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 2, 16, 2, 4, 1, 0, 0)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 8, 16, 1, 1, 4, 0, 0)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 4, 16, 1, 2, 1, 2, 1 << 30)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 0, 1, 1)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 2, 16, 2, 4, 1, 0, 0, 0)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 8, 16, 1, 1, 4, 0, 0, 0)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 4, 16, 1, 2, 1, 0, 0, 0)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 8, 16, 1, 2, 1, 1, 2, 128)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 16, 16, 1, 2, 1, 1, 129, 1 << 30)
 };
 #undef TRK_ENTRY
 #undef TRK_CFG
@@ -591,8 +742,9 @@ int mfma_register(Plan *plan) {
         v.t_min = e.t_min;
         v.t_max = e.t_max;
         v.launch = e.launch;
-        std::snprintf(v.name, sizeof(v.name), "ring3_mfma<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.F,
-                      k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
+        std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+                      k.WIDE ? "_wide" : "", k.F, k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3,
+                      k.NACC);
         ++added;
     }
     return added;

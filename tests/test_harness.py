@@ -13,9 +13,11 @@ SCRIPT = Path(__file__).resolve().parents[1] / "kernel-task_amd" / "benchmarks" 
 
 def run_harness(tmp_path, *extra):
     out = tmp_path / "results.json"
-    subprocess.run([sys.executable, str(SCRIPT), "--input-modes", "2,2,2", "--output-modes",
-                    "2,3,2", "--rank", "2", "--tokens", "1", "--warmup", "1", "--iterations", "2",
-                    "--output", str(out), *extra], check=True, capture_output=True, text=True)
+    done = subprocess.run([sys.executable, str(SCRIPT), "--input-modes", "2,2,2", "--output-modes",
+                           "2,3,2", "--rank", "2", "--tokens", "1", "--warmup", "1",
+                           "--iterations", "2", "--output", str(out), *extra],
+                          capture_output=True, text=True)
+    assert done.returncode == 0, done.stdout + done.stderr
     return json.loads(out.read_text())
 
 
