@@ -116,15 +116,18 @@ struct Geo {
     static constexpr int NSTEP = cdiv(nL, IC);
     static constexpr int NFC = cdiv(oF, FC), NSC = cdiv(oS, SC), NLC = cdiv(oL, LC);
     static constexpr int NBLK = NFC * NSC * NLC;  // workgroups per token tile
+    // LDS row pitches: 16 bytes past the K extent (a multiple of 32 bytes), so that the 16
+    // rows one MFMA fragment read touches start in 16 distinct 16-byte bank groups
+    static constexpr int PF = KF + 8, P2 = K2 + 8, P3 = K3 + 8, PL = R2 + 8;
     // LDS layout, in elements
-    static constexpr int oFs = 0, szFs = WIDE ? 8 : M1 * KF;
-    static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * K2;
+    static constexpr int oFs = 0, szFs = WIDE ? 8 : M1 * PF;
+    static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * P2;
     // WIDE: each wave holds the A fragments of BM1 stage-1 and BM2 stage-2 row tiles
     static constexpr int BM1 = cdiv(M1T, 4), BM2 = cdiv(M2T, 4);
-    static constexpr int oLs = oSs + szSs, szLs = IC * LCP * R2;
-    static constexpr int oXs = oLs + szLs, szXs = N1P * KF;
-    static constexpr int oUb = oXs + szXs, szUb = N2P * K2;
-    static constexpr int oVb = oUb + szUb, szVb = M3P * K3;
+    static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
+    static constexpr int oXs = oLs + szLs, szXs = N1P * PF;
+    static constexpr int oUb = oXs + szXs, szUb = N2P * P2;
+    static constexpr int oVb = oUb + szUb, szVb = M3P * P3;
     static constexpr int LDS_ELEMS = oVb + szVb;
     static constexpr int LDS_BYTES = LDS_ELEMS * 2;
     static constexpr int RED_FLOATS = (KS3 - 1) * G3 * NYW * 256;
@@ -156,9 +159,11 @@ __device__ inline void wait_loads() { __builtin_amdgcn_s_waitcnt(0); }
 
 // LDS <- global through VGPRs for NB blocks of BLOCK 16-byte vectors: block b is read from
 // src + b * stride (vectors), its first `valid` vectors from memory and the rest zero.
-// issue() starts every read of the copy; commit(), after wait_loads(), writes the LDS.
-template <int NB, int BLOCK>
+// issue() starts every read of the copy; commit(), after wait_loads(), writes the LDS as
+// rows of ROW vectors, each followed by one vector of pitch padding.
+template <int NB, int BLOCK, int ROW>
 struct RegCopy {
+    static_assert(BLOCK % ROW == 0, "a copy block holds whole LDS rows");
     static constexpr int TOTAL = NB * BLOCK, PER = cdiv(TOTAL, kThreads);
     uint4 r[PER];
     __device__ __forceinline__ void issue(const void *src, size_t stride, int valid) {
@@ -175,7 +180,7 @@ struct RegCopy {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int i = threadIdx.x + j * kThreads;
-            if (TOTAL % kThreads == 0 || i < TOTAL) d[i] = r[j];
+            if (TOTAL % kThreads == 0 || i < TOTAL) d[i + i / ROW] = r[j];
         }
     }
 };
@@ -216,9 +221,9 @@ constexpr Blocking choose_blocking(int MT, int NT, int KS) {
     return best;
 }
 
-// One LDS GEMM stage: D[MT*16][NT*16] = A[.][K] . B[.][K]^T (rows K-contiguous, pitch K),
+// One LDS GEMM stage: D[MT*16][NT*16] = A[.][K] . B[.][K]^T (rows K-contiguous, pitch P),
 // register-blocked as above; each finished tile goes to st(mt, nt, d).
-template <class O, int MT, int NT, int K, class Store>
+template <class O, int MT, int NT, int K, int P, class Store>
 __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename O::E *B, int wave,
                                          int lrow, int lgrp, Store &&st) {
     using V8 = typename O::V8;
@@ -232,8 +237,8 @@ __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename 
         const int blk = wave + 4 * j;
         if (BLOCKS % 4 != 0 && blk >= BLOCKS) break;
         const int m0 = (blk / NBN) * BM, n0 = (blk % NBN) * BN;
-        const typename O::E *a = A + (m0 * 16 + lrow) * K;
-        const typename O::E *b = B + (n0 * 16 + lrow) * K;
+        const typename O::E *a = A + (m0 * 16 + lrow) * P;
+        const typename O::E *b = B + (n0 * 16 + lrow) * P;
         f32x4 d[BM][BN];
 #pragma unroll
         for (int i = 0; i < BM; ++i)
@@ -245,12 +250,12 @@ __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename 
 #pragma unroll
             for (int i = 0; i < BM; ++i)
                 af[i] = (MT % BM == 0 || m0 + i < MT)
-                            ? *reinterpret_cast<const V8 *>(a + i * 16 * K + 32 * k + 8 * lgrp)
+                            ? *reinterpret_cast<const V8 *>(a + i * 16 * P + 32 * k + 8 * lgrp)
                             : V8{};
 #pragma unroll
             for (int q = 0; q < BN; ++q)
                 bf[q] = (NT % BN == 0 || n0 + q < NT)
-                            ? *reinterpret_cast<const V8 *>(b + q * 16 * K + 32 * k + 8 * lgrp)
+                            ? *reinterpret_cast<const V8 *>(b + q * 16 * P + 32 * k + 8 * lgrp)
                             : V8{};
 #pragma unroll
             for (int i = 0; i < BM; ++i)
@@ -262,12 +267,12 @@ __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename 
 #pragma unroll
             for (int i = 0; i < BM; ++i)
                 af[i] = (MT % BM == 0 || m0 + i < MT)
-                            ? *reinterpret_cast<const V4 *>(a + i * 16 * K + K - 16 + 4 * lgrp)
+                            ? *reinterpret_cast<const V4 *>(a + i * 16 * P + K - 16 + 4 * lgrp)
                             : V4{};
 #pragma unroll
             for (int q = 0; q < BN; ++q)
                 bf[q] = (NT % BN == 0 || n0 + q < NT)
-                            ? *reinterpret_cast<const V4 *>(b + q * 16 * K + K - 16 + 4 * lgrp)
+                            ? *reinterpret_cast<const V4 *>(b + q * 16 * P + K - 16 + 4 * lgrp)
                             : V4{};
 #pragma unroll
             for (int i = 0; i < BM; ++i)
@@ -309,9 +314,9 @@ struct RegA {
 };
 
 // One LDS GEMM stage with the A operand in registers (RegA, this wave's BMW row tiles): for
-// every column tile nt the wave reads the B fragments once from LDS and runs BMW MFMAs per K
-// step on them, then hands the BMW result tiles to st(nt, d).
-template <class O, int BMW, int K, int NT, class Store>
+// every column tile nt the wave reads the B fragments (LDS rows of pitch P) once and runs BMW
+// MFMAs per K step on them, then hands the BMW result tiles to st(nt, d).
+template <class O, int BMW, int K, int P, int NT, class Store>
 __device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typename O::E *B,
                                          int lrow, int lgrp, Store &&st) {
     using V8 = typename O::V8;
@@ -319,7 +324,7 @@ __device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typenam
     constexpr int K32 = K / 32, K16 = (K % 32) / 16;
 #pragma unroll 2
     for (int nt = 0; nt < NT; ++nt) {
-        const typename O::E *b = B + (nt * 16 + lrow) * K;
+        const typename O::E *b = B + (nt * 16 + lrow) * P;
         V8 b8[K32 > 0 ? K32 : 1];
         V4 b4{};
 #pragma unroll
@@ -410,12 +415,12 @@ __global__ void __launch_bounds__(kThreads)
             const int m0 = flat / (C.i1 * C.i2), m1 = (flat / C.i2) % C.i1, m2 = flat % C.i2;
             const int iF = pick(C.F, m0, m1, m2), iS = pick(C.S, m0, m1, m2);
             const int ilp = pick(C.L, m0, m1, m2) - iL0;
-            if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nS + iS) * G::KF + iF] = e[q];
+            if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nS + iS) * G::PF + iF] = e[q];
         }
     };
-    RegCopy<1, G::WIDE ? 1 : G::szFs / 8> cF;
-    RegCopy<1, G::WIDE ? 1 : G::szSs / 8> cS;
-    RegCopy<G::IC, G::LCP * R2 / 8> cL;
+    RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8> cF;
+    RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8> cS;
+    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8> cL;
     auto issue_step = [&](int iL0) {
         cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
         if constexpr (G::XROW) {
@@ -435,7 +440,7 @@ __global__ void __launch_bounds__(kThreads)
             for (int j = 0; j < XREG; ++j) {
                 const int v = tid + j * kThreads;
                 if ((G::NXV % kThreads == 0 || v < G::NXV) && t0 + (v / cpr / G::nS) % G::TT < T)
-                    *reinterpret_cast<XV *>(Xs + (v / cpr) * G::KF + (v % cpr) * G::VX) = xr[j];
+                    *reinterpret_cast<XV *>(Xs + (v / cpr) * G::PF + (v % cpr) * G::VX) = xr[j];
             }
         } else {
 #pragma unroll
@@ -468,12 +473,12 @@ __global__ void __launch_bounds__(kThreads)
     // Ub K padding).
     for (int i = tid; i < G::N1P * G::KF; i += kThreads) {
         const int n = i / G::KF, iF = i % G::KF;
-        if (iF >= G::nF || n >= G::N1 || t0 + (n / G::nS) % G::TT >= T) Xs[i] = E(0.0f);
+        if (iF >= G::nF || n >= G::N1 || t0 + (n / G::nS) % G::TT >= T) Xs[n * G::PF + iF] = E(0.0f);
     }
     if constexpr (G::K2 > G::nS * R) {
         constexpr int pad = G::K2 - G::nS * R;
         for (int i = tid; i < G::N2P * pad; i += kThreads)
-            Ub[(i / pad) * G::K2 + G::nS * R + i % pad] = E(0.0f);
+            Ub[(i / pad) * G::P2 + G::nS * R + i % pad] = E(0.0f);
     }
     commit_step(0);
     if constexpr (!G::WIDE) {
@@ -505,18 +510,18 @@ __global__ void __launch_bounds__(kThreads)
         // stage 1: U^T = F . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]. The Ub offset of an entry is
         // a row part (r1, f, r2) plus a column part (iL', t, iS).
         auto ub_row = [&](int m0) {
-            return ((m0 / R) % R * G::TT * G::FC + m0 / R2) * G::K2 + m0 % R;
+            return ((m0 / R) % R * G::TT * G::FC + m0 / R2) * G::P2 + m0 % R;
         };
         auto ub_col = [&](int n) {
             const int iS = n % G::nS, t = (n / G::nS) % G::TT, ilp = n / (G::nS * G::TT);
-            return (ilp * R * G::TT * G::FC + t * G::FC) * G::K2 + iS * R;
+            return (ilp * R * G::TT * G::FC + t * G::FC) * G::P2 + iS * R;
         };
         auto put4 = [&](E *dst, f32x4 d) {
             E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
             *reinterpret_cast<E4 *>(dst) = h;
         };
         if constexpr (G::WIDE) {
-            reg_gemm<O, G::BM1, G::KF, G::N1T>(fa, Xs, lrow, lgrp, [&](int nt, const f32x4 *d) {
+            reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T>(fa, Xs, lrow, lgrp, [&](int nt, const f32x4 *d) {
                 const int n = nt * 16 + lrow;
                 if (G::N1 % 16 != 0 && n >= G::N1) return;
                 const int col = ub_col(n);
@@ -527,7 +532,7 @@ __global__ void __launch_bounds__(kThreads)
                 }
             });
         } else {
-            lds_gemm<O, G::M1T, G::N1T, G::KF>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            lds_gemm<O, G::M1T, G::N1T, G::KF, G::PF>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
                 const int n = nt * 16 + lrow;
                 if (G::N1 % 16 == 0 || n < G::N1) put4(Ub + ub_col(n) + ub_row(mt * 16 + 4 * lgrp), d);
             });
@@ -536,14 +541,14 @@ __global__ void __launch_bounds__(kThreads)
 
         // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)]: row part (s, r3), column part
         // (iL', r1, t, f)
-        auto vb_row = [&](int m0) { return (m0 / R) * G::K3 + m0 % R; };
+        auto vb_row = [&](int m0) { return (m0 / R) * G::P3 + m0 % R; };
         auto vb_col = [&](int n) {
             const int f = n % G::FC, t = (n / G::FC) % G::TT, r1 = (n / (G::FC * G::TT)) % R;
             const int ilp = n / (G::FC * G::TT * R);
-            return (t * G::FC + f) * G::SC * G::K3 + (ilp * R + r1) * R;
+            return (t * G::FC + f) * G::SC * G::P3 + (ilp * R + r1) * R;
         };
         if constexpr (G::WIDE) {
-            reg_gemm<O, G::BM2, G::K2, G::N2T>(sa, Ub, lrow, lgrp, [&](int nt, const f32x4 *d) {
+            reg_gemm<O, G::BM2, G::K2, G::P2, G::N2T>(sa, Ub, lrow, lgrp, [&](int nt, const f32x4 *d) {
                 const int n = nt * 16 + lrow;
                 if (G::N2 % 16 != 0 && n >= G::N2) return;
                 const int col = vb_col(n);
@@ -554,7 +559,7 @@ __global__ void __launch_bounds__(kThreads)
                 }
             });
         } else {
-            lds_gemm<O, G::M2T, G::N2T, G::K2>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            lds_gemm<O, G::M2T, G::N2T, G::K2, G::P2>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
                 const int n = nt * 16 + lrow;
                 const int m0 = mt * 16 + 4 * lgrp;
                 if ((G::N2 % 16 == 0 || n < G::N2) && (G::M2 % 16 == 0 || m0 < G::M2))
@@ -572,7 +577,7 @@ __global__ void __launch_bounds__(kThreads)
             const int tile = g3 + G::G3 * j;
             if (G::NT3 % G::G3 == 0 || tile < G::NT3) {
                 const int mt = tile / G::N3T, nt = tile % G::N3T;
-                const E *a = Vb + (mt * 16 + lrow) * G::K3;
+                const E *a = Vb + (mt * 16 + lrow) * G::P3;
                 const int l = nt * 16 + lrow;
 #pragma unroll
                 for (int q0 = 0; q0 < PERK; q0 += QB) {
@@ -582,7 +587,7 @@ __global__ void __launch_bounds__(kThreads)
                         const int k = (part3 * PERK + q0 + q) * 32;
                         af[q] = *reinterpret_cast<const typename O::V8 *>(a + k + 8 * lgrp);
                         bf[q] = *reinterpret_cast<const typename O::V8 *>(
-                            Ls + ((k / R2) * G::LCP + l) * R2 + k % R2 + 8 * lgrp);
+                            Ls + ((k / R2) * G::LCP + l) * G::PL + k % R2 + 8 * lgrp);
                     }
 #pragma unroll
                     for (int q = 0; q < QB; ++q)
@@ -707,7 +712,6 @@ const Entry kEntries[] = {
     // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 0, 1, 1)
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 2, 16, 2, 4, 1, 0, 0, 0)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 8, 16, 1, 1, 4, 0, 0, 0)
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 4, 16, 1, 2, 1, 0, 0, 0)
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 8, 16, 1, 2, 1, 1, 2, 128)
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 16, 16, 1, 2, 1, 1, 129, 1 << 30)
