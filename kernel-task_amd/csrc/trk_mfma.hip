@@ -313,34 +313,54 @@ struct RegA {
     }
 };
 
-// One LDS GEMM stage with the A operand in registers (RegA, this wave's BMW row tiles): for
-// every column tile nt the wave reads the B fragments (LDS rows of pitch P) once and runs BMW
-// MFMAs per K step on them, then hands the BMW result tiles to st(nt, d).
+// One LDS GEMM stage with the A operand in registers (RegA, this wave's BMW row tiles). The
+// NT column tiles go in blocks of BN: per K step the wave reads the block's BN B fragments
+// (LDS rows of pitch P) and runs BMW x BN independent MFMAs on them, so the next step's reads
+// overlap this step's MFMAs. Each finished column tile goes to st(nt, d[BMW]).
 template <class O, int BMW, int K, int P, int NT, class Store>
 __device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typename O::E *B,
                                          int lrow, int lgrp, Store &&st) {
     using V8 = typename O::V8;
     using V4 = typename O::V4;
     constexpr int K32 = K / 32, K16 = (K % 32) / 16;
-#pragma unroll 2
-    for (int nt = 0; nt < NT; ++nt) {
-        const typename O::E *b = B + (nt * 16 + lrow) * P;
-        V8 b8[K32 > 0 ? K32 : 1];
-        V4 b4{};
+    constexpr int BN0 = 16 / BMW < 1 ? 1 : 16 / BMW;  // at most 16 accumulator tiles
+    constexpr int BN = BN0 < NT ? BN0 : NT;
 #pragma unroll
-        for (int k = 0; k < K32; ++k) b8[k] = *reinterpret_cast<const V8 *>(b + 32 * k + 8 * lgrp);
-        if constexpr (K16) b4 = *reinterpret_cast<const V4 *>(b + K - 16 + 4 * lgrp);
-        f32x4 d[BMW];
+    for (int n0 = 0; n0 < NT; n0 += BN) {
+        const typename O::E *b = B + (n0 * 16 + lrow) * P;
+        f32x4 d[BN][BMW];
 #pragma unroll
-        for (int i = 0; i < BMW; ++i) d[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q = 0; q < BN; ++q)
 #pragma unroll
-        for (int k = 0; k < K32; ++k)
+            for (int i = 0; i < BMW; ++i) d[q][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < BMW; ++i) d[i] = O::k32(A.a8[i][k], b8[k], d[i]);
-        if constexpr (K16)
+        for (int k = 0; k < K32; ++k) {
+            V8 bf[BN];
 #pragma unroll
-            for (int i = 0; i < BMW; ++i) d[i] = O::k16(A.a4[i], b4, d[i]);
-        st(nt, d);
+            for (int q = 0; q < BN; ++q)
+                if (NT % BN == 0 || n0 + q < NT)
+                    bf[q] = *reinterpret_cast<const V8 *>(b + q * 16 * P + 32 * k + 8 * lgrp);
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                if (NT % BN == 0 || n0 + q < NT)
+#pragma unroll
+                    for (int i = 0; i < BMW; ++i) d[q][i] = O::k32(A.a8[i][k], bf[q], d[q][i]);
+        }
+        if constexpr (K16) {
+            V4 bf[BN];
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                if (NT % BN == 0 || n0 + q < NT)
+                    bf[q] = *reinterpret_cast<const V4 *>(b + q * 16 * P + K - 16 + 4 * lgrp);
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                if (NT % BN == 0 || n0 + q < NT)
+#pragma unroll
+                    for (int i = 0; i < BMW; ++i) d[q][i] = O::k16(A.a4[i], bf[q], d[q][i]);
+        }
+#pragma unroll
+        for (int q = 0; q < BN; ++q)
+            if (NT % BN == 0 || n0 + q < NT) st(n0 + q, d[q]);
     }
 }
 
@@ -684,7 +704,10 @@ constexpr int H = TRK_DTYPE_F16, B = TRK_DTYPE_BF16;
 // WIDE, default token range (0 0: reachable by index only)
 const Entry kEntries[] = {
     // 1920 -> 2880, (8,12,20) -> (12,10,24), rank 8, fp16
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 1, 4, 0, 1, 1)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 1, 4, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 4, 1, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 4, 1, 1, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 2, 2, 0, 1, 1)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 1, 12, 8, 1, 4, 0, 0, 0)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 5, 12, 8, 1, 4, 0, 0, 0)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 0, 0, 0)
@@ -693,16 +716,20 @@ const Entry kEntries[] = {
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 1, 2, 1 << 30)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 4, 1, 10, 12, 4, 2, 1, 1, 0, 0)
     // same modes, rank 16, fp16
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 2, 2, 0, 1, 1)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 2, 2, 0, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 4, 1, 0, 1, 1)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 4, 1, 1, 0, 0)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 2, 12, 4, 4, 1, 0, 0, 0)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 5, 12, 4, 1, 4, 0, 0, 0)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 0, 0, 0)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 5, 12, 2, 2, 1, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 1, 2, 1 << 30)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 10, 12, 2, 2, 1, 1, 0, 0)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 1, 2, 24)
+    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 10, 12, 2, 2, 1, 1, 25, 1 << 30)
     TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 2, 1, 10, 12, 4, 1, 4, 1, 0, 0)
     // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16
     TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 2, 2, 0, 1, 1)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 4, 1, 0, 0, 0)
+    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 4, 1, 1, 0, 0)
     TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 4, 32, 8, 2, 2, 0, 0, 0)
     TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 7, 32, 8, 1, 2, 0, 0, 0)
     TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 14, 32, 8, 1, 2, 0, 2, 8)
@@ -711,6 +738,7 @@ const Entry kEntries[] = {
     TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 4, 1, 28, 32, 4, 1, 2, 1, 65, 1 << 30)
     // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 0, 1, 1)
+    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 1, 0, 0)
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 2, 16, 2, 4, 1, 0, 0, 0)
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 4, 16, 1, 2, 1, 0, 0, 0)
     TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 8, 16, 1, 2, 1, 1, 2, 128)

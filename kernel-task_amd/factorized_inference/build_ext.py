@@ -19,6 +19,7 @@ CSRC = PACKAGE.parent / "csrc"
 INCLUDE = PACKAGE.parents[1] / "include"
 LIBRARY = PACKAGE / "libtrk.so"
 FASTCALL = PACKAGE / ("_trkcall" + sysconfig.get_config_var("EXT_SUFFIX"))
+TORCHCALL = PACKAGE / ("_trktorch" + sysconfig.get_config_var("EXT_SUFFIX"))
 OBJ_DIR = PACKAGE.parent / "_build"
 ARCH = "gfx950"
 
@@ -73,7 +74,30 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
+    _build_torchcall(verbose)
     return LIBRARY
+
+
+def _build_torchcall(verbose: bool) -> None:
+    """_trktorch: PreparedTRKernel's per-call path in C++ (g++ against torch's headers)."""
+    import torch
+
+    root = Path(torch.__file__).resolve().parent
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch.compiled_with_cxx11_abi())}",
+           f"-I{root / 'include'}", f"-I{root / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+           f"-I{rocm}/include", f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
+           str(CSRC / "trk_torchcall.cpp"), "-o", str(TORCHCALL.with_suffix(".tmp")),
+           f"-L{root / 'lib'}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_python",
+           f"-L{PACKAGE}", "-l:libtrk.so", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    done = subprocess.run(cmd, capture_output=True, text=True)
+    if done.returncode != 0:
+        raise RuntimeError(f"g++ failed on trk_torchcall.cpp:\n{done.stderr}")
+    os.replace(TORCHCALL.with_suffix(".tmp"), TORCHCALL)
 
 
 if __name__ == "__main__":

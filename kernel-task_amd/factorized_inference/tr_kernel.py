@@ -5,9 +5,11 @@ prepare time, a tiling/variant choice per token count) with its own mechanics:
 
   prepare  trk_plan_create picks the contraction order(s) and kernel variants for the shape;
            trk_pack packs the cores into one device buffer (no dense W, padding only)
-  call     one C call per input: trk_forward on the caller's current stream, writing a
-           fresh output tensor. No workspace, counters or other state survives a call, so
-           one prepared object may be used from several streams.
+  call     one C++ call per input (_trktorch.forward): check x, allocate the output with
+           torch's caching allocator, trk_forward on the caller's current stream. No
+           workspace, counters or other state survives a call, so one prepared object may
+           be used from several streams. Inputs that need checking or copying go through
+           the Python path below, which raises or copies first.
 
 Environment switch (read at prepare time, for sweeps): TRK_VARIANT=<index> routes every
 token count to that variant of the plan (indices from `PreparedTRKernel.variants()`).
@@ -39,6 +41,18 @@ def _fast_forward():
         lib = _lib.load()
         return lib.trk_forward, lib.trk_forward_variant
     return _trkcall.forward, _trkcall.forward_variant
+
+
+def _torch_call():
+    """_trktorch (built next to libtrk.so): PreparedTRKernel's per-call path in C++."""
+    _lib.load()
+    try:
+        from . import _trktorch
+    except ImportError as exc:
+        raise RuntimeError(
+            f"the _trktorch extension is not built or does not load ({exc}); run "
+            "python -m factorized_inference.build_ext") from exc
+    return _trktorch
 
 
 def current_stream_handle(device_index: int) -> int:
@@ -82,6 +96,10 @@ class PreparedTRKernel:
         self._forward, self._forward_variant = _fast_forward()
         self._plan_handle = self.plan.handle
         self._packed_ptr = self.packed.data_ptr()
+        torch_call = _torch_call()
+        self._bound = torch_call.bind(self._plan_handle, self._packed_ptr, self.in_features,
+                                      self.out_features, _DTYPES[dtype], self.device_index)
+        self._call = torch_call.forward
 
     # ---- queries -------------------------------------------------------------------------
     @property
@@ -102,11 +120,17 @@ class PreparedTRKernel:
         if x.ndim != 2 or x.shape[1] != self.in_features:
             raise ValueError(
                 f"Expected x with shape [tokens, {self.in_features}], got {tuple(x.shape)}")
+        if x.shape[0] > 2**31 - 1:
+            raise ValueError(f"At most 2**31 - 1 tokens per call, got {x.shape[0]}")
         if not x.is_contiguous() or x.data_ptr() & 15:
             x = x.clone(memory_format=torch.contiguous_format)
         return x
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        y = self._call(self._bound, x)
+        return y if y is not None else self._checked_call(x)
+
+    def _checked_call(self, x: torch.Tensor) -> torch.Tensor:
         x = self._check(x)
         tokens = x.shape[0]
         y = x.new_empty((tokens, self.out_features))

@@ -147,6 +147,23 @@ def test_library_exports_every_declared_symbol():
     assert lib.trk_empty_call() == 0
 
 
+def test_call_bindings_load_and_check_their_arguments():
+    from factorized_inference import _trkcall, _trktorch
+
+    assert callable(_trkcall.forward) and callable(_trkcall.forward_variant)
+    plan = _lib.Plan((2, 3, 2), (2, 4, 3), 2, _lib.DTYPE_F16)
+    with pytest.raises(ValueError, match="null plan"):
+        _trktorch.bind(0, 0, 12, 24, _lib.DTYPE_F16, 0)
+    with pytest.raises(ValueError, match="unknown dtype"):
+        _trktorch.bind(plan.handle, 256, 12, 24, 7, 0)
+    bound = _trktorch.bind(plan.handle, 256, 12, 24, _lib.DTYPE_F16, 0)
+    # inputs the C++ path does not take come back as None (no launch happens for them)
+    assert _trktorch.forward(bound, torch.zeros(1, 12, dtype=torch.float16)) is None
+    assert _trktorch.forward(bound, "not a tensor") is None
+    with pytest.raises(TypeError):
+        _trktorch.forward(bound)
+
+
 @pytest.mark.parametrize("ins,outs,R,dtype", [
     ((8, 12, 20), (12, 10, 24), 8, _lib.DTYPE_F16),
     ((8, 12, 20), (12, 10, 24), 16, _lib.DTYPE_F16),
