@@ -26,6 +26,11 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
+# Kernel arguments in host memory: the HIP runtime's default on this GPU copies them to device
+# memory and reads them back before each launch, which costs ~1.5 us of host time per launch
+# with arguments (every launch measured here, ours and the dense GEMM alike). Set before HIP
+# initialises; an explicit setting in the environment wins.
+os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "0")
 sys.path.insert(0, str(ROOT / "kernel-task_amd"))
 sys.path.insert(0, str(ROOT))
 
@@ -231,7 +236,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "tensor-ring linear 1920->2880, modes (8,12,20)->(12,10,24), "
                                "rank 8, fp16, tokens 1 (BASELINE configs[1])",
-                   "tokens": 1, "rank": 8, "in_features": 1920, "out_features": 2880},
+                   "tokens": 1, "rank": 8, "in_features": 1920, "out_features": 2880,
+                   "hip_force_dev_kernarg": os.environ.get("HIP_FORCE_DEV_KERNARG")},
         "dense_stream_us": head["dense_stream_us"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": m.PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / m.PEAK_HBM_GBS, "traffic": traffic,

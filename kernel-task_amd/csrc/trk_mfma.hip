@@ -26,6 +26,7 @@
 // other shapes use the generic kernel (trk_generic.hip).
 #include <algorithm>
 #include <cstdio>
+#include <type_traits>
 
 #include "trk_internal.h"
 
@@ -33,6 +34,7 @@ namespace trk {
 namespace {
 
 using f32x4 = float __attribute__((ext_vector_type(4)));
+using f32x16 = float __attribute__((ext_vector_type(16)));
 
 template <int DT>
 struct Ops;
@@ -49,6 +51,9 @@ struct Ops<TRK_DTYPE_F16> {
     __device__ static f32x4 k16(V4 a, V4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
     }
+    __device__ static f32x16 w16(V8 a, V8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
 };
 
 template <>
@@ -62,6 +67,9 @@ struct Ops<TRK_DTYPE_BF16> {
     }
     __device__ static f32x4 k16(V4 a, V4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
+    __device__ static f32x16 w16(V8 a, V8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
 };
 
@@ -79,7 +87,11 @@ struct KCfg {
     int TT, FC, SC, LC, IC;  // tokens, f / s / l digits per workgroup, iL digits per step
     int KS3;                 // waves sharing one stage-3 tile (split of its K range)
     int NACC;                // independent accumulator chains per stage-3 tile and wave
-    int WIDE;                // 1: first/second-core slices held in registers, not LDS
+    int WIDE;                // 0: core slices in LDS. 1, 2 or 4: the first- and second-core
+                             // slices live in registers, and WIDE waves split the stage-2
+                             // rows while 4 / WIDE waves split its columns
+    int MF2;                 // WIDE stage-2 MFMA: 16 (16x16x32) or 32 (32x32x16, twice the
+                             // matrix-core throughput of 16x16x32 on gfx950)
 };
 
 template <KCfg C>
@@ -102,9 +114,12 @@ struct Geo {
     static constexpr int TT = C.TT, FC = C.FC, SC = C.SC, LC = C.LC, IC = C.IC, KS3 = C.KS3;
     static constexpr int NACC = C.NACC;
     static constexpr bool WIDE = C.WIDE != 0;
-    // stage 1: A = Fs [M1][KF], B = Xs [N1P][KF]
+    // stage 1: A = Fs [M1][KF], B = Xs [N1][KF]. The B rows are (iL', t, iS) with iS padded
+    // to nSP, a multiple of 16, so that every 16-row tile has one (iL', t) and its stores
+    // go to a per-tile constant plus a per-lane constant offset.
+    static constexpr int nSP = rup(nS, 16);
     static constexpr int M1 = FC * R2, M1T = M1 / 16;
-    static constexpr int N1 = IC * TT * nS, N1T = cdiv(N1, 16), N1P = N1T * 16;
+    static constexpr int N1 = IC * TT * nSP, N1T = N1 / 16, N1P = N1;
     // stage 2: A = Ss [M2P][K2], B = Ub [N2P][K2]
     static constexpr int M2 = SC * R, M2T = cdiv(M2, 16), M2P = M2T * 16;
     static constexpr int N2 = IC * R * TT * FC, N2T = cdiv(N2, 16), N2P = N2T * 16;
@@ -122,11 +137,16 @@ struct Geo {
     // LDS layout, in elements
     static constexpr int oFs = 0, szFs = WIDE ? 8 : M1 * PF;
     static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * P2;
-    // WIDE: each wave holds the A fragments of BM1 stage-1 and BM2 stage-2 row tiles
-    static constexpr int BM1 = cdiv(M1T, 4), BM2 = cdiv(M2T, 4);
+    // WIDE: each wave holds the A fragments of BM1 stage-1 and BM2 stage-2 row tiles; stage 2
+    // runs on a WM2 x WN2 grid of waves (rows x columns)
+    static constexpr int WM2 = WIDE ? C.WIDE : 4, WN2 = 4 / WM2;
+    static constexpr bool W32 = WIDE && C.MF2 == 32;  // stage 2 on 32x32 tiles
+    static constexpr int M2T32 = cdiv(M2, 32), N2T32 = cdiv(N2, 32);
+    static constexpr int BM1 = cdiv(M1T, 4), BM2 = cdiv(W32 ? M2T32 : M2T, WM2);
+    static constexpr int N2R = W32 ? N2T32 * 32 : N2P;  // Ub rows (the last tile's padding)
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
     static constexpr int oXs = oLs + szLs, szXs = N1P * PF;
-    static constexpr int oUb = oXs + szXs, szUb = N2P * P2;
+    static constexpr int oUb = oXs + szXs, szUb = N2R * P2;
     static constexpr int oVb = oUb + szUb, szVb = M3P * P3;
     static constexpr int LDS_ELEMS = oVb + szVb;
     static constexpr int LDS_BYTES = LDS_ELEMS * 2;
@@ -138,11 +158,15 @@ struct Geo {
         return nF % v == 0 && SXS % v == 0 && SXL % v == 0 && IN % v == 0;
     }
     static constexpr int VX = !XROW ? 1 : vx_fits(8) ? 8 : vx_fits(4) ? 4 : vx_fits(2) ? 2 : 1;
-    static constexpr int NXV = IC * TT * nS * (nF / VX);     // vectors per step (contiguous iF)
+    static constexpr int XCPR = KF / VX;                      // vectors per Xs row (contiguous iF)
+    static constexpr int NXV = N1 * XCPR;                     // vectors per step (contiguous iF)
     static constexpr int NXB = TT * IN / 8;                   // vectors per step (scatter)
     static constexpr int XB = 8;
 
-    static_assert(R % 8 == 0, "MFMA variants need a rank that is a multiple of 8");
+    static_assert(R % 8 == 0 && (R & (R - 1)) == 0, "MFMA variants need a power-of-two rank >= 8");
+    static_assert(C.WIDE == 0 || C.WIDE == 1 || C.WIDE == 2 || C.WIDE == 4, "WIDE is 0, 1, 2 or 4");
+    static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
+    static_assert(16 % (FC * TT) == 0, "FC * TT must divide 16 (stage-2 store offsets)");
     static_assert(KS3 == 1 || KS3 == 2 || KS3 == 4, "KS3 must divide the 4 waves");
     static_assert(NACC >= 1 && (K3 / 32 / KS3) % NACC == 0, "NACC must divide a wave's K steps");
     static_assert(FC <= oF && SC <= oS && LC <= oL && IC <= nL && TT >= 1, "tile too large");
@@ -313,54 +337,147 @@ struct RegA {
     }
 };
 
-// One LDS GEMM stage with the A operand in registers (RegA, this wave's BMW row tiles). The
-// NT column tiles go in blocks of BN: per K step the wave reads the block's BN B fragments
-// (LDS rows of pitch P) and runs BMW x BN independent MFMAs on them, so the next step's reads
-// overlap this step's MFMAs. Each finished column tile goes to st(nt, d[BMW]).
-template <class O, int BMW, int K, int P, int NT, class Store>
-__device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typename O::E *B,
+// One LDS GEMM stage with the A operand in registers (RegA, this wave's BMW row tiles) over
+// the column tiles nt = wn, wn + WN, ... below NT. They go in blocks of BN; per K step the
+// wave runs BMW x BN independent MFMAs on the block's BN B fragments (LDS rows of pitch P)
+// while the fragments of the next K step are already being read (two register buffers,
+// kept in that order by scheduling barriers). Each finished column tile goes to
+// st(nt, d[BMW]).
+template <class O, int BMW, int K, int P, int NT, int WN, class Store>
+__device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typename O::E *B, int wn,
                                          int lrow, int lgrp, Store &&st) {
     using V8 = typename O::V8;
     using V4 = typename O::V4;
     constexpr int K32 = K / 32, K16 = (K % 32) / 16;
-    constexpr int BN0 = 16 / BMW < 1 ? 1 : 16 / BMW;  // at most 16 accumulator tiles
-    constexpr int BN = BN0 < NT ? BN0 : NT;
+    constexpr int NTW = cdiv(NT, WN);                     // column tiles per wave (at most)
+    constexpr int BN0 = 16 / BMW < 1 ? 1 : 16 / BMW;      // at most 16 accumulator tiles
+    constexpr int BN = BN0 < NTW ? BN0 : NTW;
 #pragma unroll
-    for (int n0 = 0; n0 < NT; n0 += BN) {
-        const typename O::E *b = B + (n0 * 16 + lrow) * P;
+    for (int j0 = 0; j0 < NTW; j0 += BN) {
+        // column tile q of the block is nt = wn + WN * (j0 + q); absent when nt >= NT
+        auto have = [&](int q) { return j0 + q < NTW && (NT % WN == 0 || wn + WN * (j0 + q) < NT); };
+        const typename O::E *b = B + ((wn + WN * j0) * 16 + lrow) * P;
+        auto frag8 = [&](int q, int k) {
+            return *reinterpret_cast<const V8 *>(b + q * WN * 16 * P + 32 * k + 8 * lgrp);
+        };
         f32x4 d[BN][BMW];
 #pragma unroll
         for (int q = 0; q < BN; ++q)
 #pragma unroll
             for (int i = 0; i < BMW; ++i) d[q][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        V8 cur[BN], nxt[BN];
+        if constexpr (K32 > 0) {
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                if (have(q)) cur[q] = frag8(q, 0);
+        }
 #pragma unroll
         for (int k = 0; k < K32; ++k) {
-            V8 bf[BN];
+            if (k + 1 < K32) {
+#pragma unroll
+                for (int q = 0; q < BN; ++q)
+                    if (have(q)) nxt[q] = frag8(q, k + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int q = 0; q < BN; ++q)
-                if (NT % BN == 0 || n0 + q < NT)
-                    bf[q] = *reinterpret_cast<const V8 *>(b + q * 16 * P + 32 * k + 8 * lgrp);
+                if (have(q))
 #pragma unroll
-            for (int q = 0; q < BN; ++q)
-                if (NT % BN == 0 || n0 + q < NT)
+                    for (int i = 0; i < BMW; ++i) d[q][i] = O::k32(A.a8[i][k], cur[q], d[q][i]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int i = 0; i < BMW; ++i) d[q][i] = O::k32(A.a8[i][k], bf[q], d[q][i]);
+            for (int q = 0; q < BN; ++q) cur[q] = nxt[q];
         }
         if constexpr (K16) {
             V4 bf[BN];
 #pragma unroll
             for (int q = 0; q < BN; ++q)
-                if (NT % BN == 0 || n0 + q < NT)
-                    bf[q] = *reinterpret_cast<const V4 *>(b + q * 16 * P + K - 16 + 4 * lgrp);
+                if (have(q))
+                    bf[q] = *reinterpret_cast<const V4 *>(b + q * WN * 16 * P + K - 16 + 4 * lgrp);
 #pragma unroll
             for (int q = 0; q < BN; ++q)
-                if (NT % BN == 0 || n0 + q < NT)
+                if (have(q))
 #pragma unroll
                     for (int i = 0; i < BMW; ++i) d[q][i] = O::k16(A.a4[i], bf[q], d[q][i]);
         }
 #pragma unroll
         for (int q = 0; q < BN; ++q)
-            if (NT % BN == 0 || n0 + q < NT) st(n0 + q, d[q]);
+            if (have(q)) st(wn + WN * (j0 + q), d[q]);
+    }
+}
+
+// A operand of 32x32x16 MFMAs held in registers: BMW 32-row tiles (rows row0 + i*32 + lane%32)
+// over K (a multiple of 16), lane holding K elements 16*s + 8*(lane/32) .. +8 of its row for
+// each K step s, read once from a K-contiguous global matrix (rows at or past `rows` zero).
+template <class O, int BMW, int K>
+struct RegA32 {
+    static_assert(K % 16 == 0, "32x32x16 fragments need K a multiple of 16");
+    typename O::V8 a[BMW][K / 16];
+    __device__ __forceinline__ void load(const typename O::E *__restrict__ src, int row0, int rows,
+                                         int lane) {
+#pragma unroll
+        for (int i = 0; i < BMW; ++i) {
+            const int row = row0 + i * 32 + (lane & 31);
+            const typename O::E *p = src + size_t(row) * K + 8 * (lane >> 5);
+#pragma unroll
+            for (int k = 0; k < K / 16; ++k)
+                a[i][k] = row < rows ? *reinterpret_cast<const typename O::V8 *>(p + 16 * k)
+                                     : typename O::V8{};
+        }
+    }
+};
+
+// reg_gemm on 32x32 tiles: A in registers (RegA32, BMW row tiles), the column tiles
+// nt = wn, wn + WN, ... below NT (32 columns each) in blocks of BN, B fragments read from
+// LDS rows of pitch P (lane: row nt*32 + lane%32, K elements 16*s + 8*(lane/32) .. +8), the
+// next K step's fragments read while this step's MFMAs run. st(nt, d[BMW]) gets each
+// finished column tile; d[i][4*g + e] is row 8*g + 4*(lane/32) + e, column lane%32.
+template <class O, int BMW, int K, int P, int NT, int WN, class Store>
+__device__ __forceinline__ void reg_gemm32(const RegA32<O, BMW, K> &A, const typename O::E *B,
+                                           int wn, int lane, Store &&st) {
+    using V8 = typename O::V8;
+    constexpr int KS = K / 16;
+    constexpr int NTW = cdiv(NT, WN);
+    constexpr int BN0 = 4 / BMW < 1 ? 1 : 4 / BMW;  // at most 4 accumulator tiles (64 VGPRs)
+    constexpr int BN = BN0 < NTW ? BN0 : NTW;
+#pragma unroll
+    for (int j0 = 0; j0 < NTW; j0 += BN) {
+        auto have = [&](int q) { return j0 + q < NTW && (NT % WN == 0 || wn + WN * (j0 + q) < NT); };
+        const typename O::E *b = B + ((wn + WN * j0) * 32 + (lane & 31)) * P + 8 * (lane >> 5);
+        auto frag = [&](int q, int k) {
+            return *reinterpret_cast<const V8 *>(b + q * WN * 32 * P + 16 * k);
+        };
+        f32x16 d[BN][BMW];
+#pragma unroll
+        for (int q = 0; q < BN; ++q)
+#pragma unroll
+            for (int i = 0; i < BMW; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) d[q][i][e] = 0.0f;
+        V8 cur[BN], nxt[BN];
+#pragma unroll
+        for (int q = 0; q < BN; ++q)
+            if (have(q)) cur[q] = frag(q, 0);
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            if (k + 1 < KS) {
+#pragma unroll
+                for (int q = 0; q < BN; ++q)
+                    if (have(q)) nxt[q] = frag(q, k + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                if (have(q))
+#pragma unroll
+                    for (int i = 0; i < BMW; ++i) d[q][i] = O::w16(A.a[i][k], cur[q], d[q][i]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < BN; ++q) cur[q] = nxt[q];
+        }
+#pragma unroll
+        for (int q = 0; q < BN; ++q)
+            if (have(q)) st(wn + WN * (j0 + q), d[q]);
     }
 }
 
@@ -386,7 +503,8 @@ __global__ void __launch_bounds__(kThreads)
     __shared__ __attribute__((aligned(16))) E Ub[G::szUb];
     __shared__ __attribute__((aligned(16))) E Vb[G::szVb];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 15, lgrp = lane >> 4;
 
     // Workgroups are dealt round-robin to the 8 XCDs, each with its own L2. Renumber them so
@@ -409,12 +527,15 @@ __global__ void __launch_bounds__(kThreads)
     constexpr int XREG = G::XROW ? XPER : (XPER < G::XB ? XPER : G::XB);
     XV xr[G::XROW ? XREG : 1];
     uint4 xb[G::XROW ? 1 : XREG];
-    auto x_row_load = [&](int v, int iL0) {  // contiguous-iF loader: vector v of the step
-        constexpr int cpr = G::nF / G::VX;
-        const int n = v / cpr, c = v % cpr;
-        const int iS = n % G::nS, t = (n / G::nS) % G::TT, iL = iL0 + n / (G::nS * G::TT);
+    // contiguous-iF loader: vector v of the step covers Xs[n][c*VX, c*VX+VX) of row
+    // n = (iL', t, iS); what lies outside x (K padding, iS >= nS, absent tokens) is zero, so
+    // these vectors write every element of Xs[:, 0:KF)
+    auto x_row_load = [&](int v, int iL0) {
+        const int n = v / G::XCPR, c = v % G::XCPR;
+        const int iS = n % G::nSP, t = (n / G::nSP) % G::TT, iL = iL0 + n / (G::nSP * G::TT);
         XV r{};
-        if ((G::NXV % kThreads == 0 || v < G::NXV) && t0 + t < T)
+        if ((G::NXV % kThreads == 0 || v < G::NXV) && c * G::VX < G::nF && iS < G::nS &&
+            t0 + t < T)
             r = *reinterpret_cast<const XV *>(x + size_t(t0 + t) * G::IN + iS * G::SXS +
                                               iL * G::SXL + c * G::VX);
         return r;
@@ -435,7 +556,7 @@ __global__ void __launch_bounds__(kThreads)
             const int m0 = flat / (C.i1 * C.i2), m1 = (flat / C.i2) % C.i1, m2 = flat % C.i2;
             const int iF = pick(C.F, m0, m1, m2), iS = pick(C.S, m0, m1, m2);
             const int ilp = pick(C.L, m0, m1, m2) - iL0;
-            if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nS + iS) * G::PF + iF] = e[q];
+            if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nSP + iS) * G::PF + iF] = e[q];
         }
     };
     RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8> cF;
@@ -455,12 +576,12 @@ __global__ void __launch_bounds__(kThreads)
         wait_loads();
         cL.commit(Ls);
         if constexpr (G::XROW) {
-            constexpr int cpr = G::nF / G::VX;
 #pragma unroll
             for (int j = 0; j < XREG; ++j) {
                 const int v = tid + j * kThreads;
-                if ((G::NXV % kThreads == 0 || v < G::NXV) && t0 + (v / cpr / G::nS) % G::TT < T)
-                    *reinterpret_cast<XV *>(Xs + (v / cpr) * G::PF + (v % cpr) * G::VX) = xr[j];
+                if (G::NXV % kThreads == 0 || v < G::NXV)
+                    *reinterpret_cast<XV *>(Xs + (v / G::XCPR) * G::PF + (v % G::XCPR) * G::VX) =
+                        xr[j];
             }
         } else {
 #pragma unroll
@@ -480,24 +601,36 @@ __global__ void __launch_bounds__(kThreads)
 
     // the first- and second-core slices stay resident for the whole call
     RegA<O, G::BM1, G::KF> fa;
-    RegA<O, G::BM2, G::K2> sa;
+    std::conditional_t<G::W32, RegA32<O, G::BM2, G::K2>, RegA<O, G::BM2, G::K2>> sa;
     if constexpr (G::WIDE) {
         fa.load(Fk + size_t(f0) * R2 * G::KF, wave * G::BM1 * 16, FCv * R2, lrow, lgrp);
-        sa.load(Sk + size_t(s0) * R * G::K2, wave * G::BM2 * 16, SCv * R, lrow, lgrp);
+        if constexpr (G::W32)
+            sa.load(Sk + size_t(s0) * R * G::K2, (wave % G::WM2) * G::BM2 * 32, SCv * R, lane);
+        else
+            sa.load(Sk + size_t(s0) * R * G::K2, (wave % G::WM2) * G::BM2 * 16, SCv * R, lrow, lgrp);
     } else {
         cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
         cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
     }
     issue_step(0);
-    // While the loads fly: zero what no load writes (Xs K padding, Xs rows of absent tokens,
-    // Ub K padding).
-    for (int i = tid; i < G::N1P * G::KF; i += kThreads) {
-        const int n = i / G::KF, iF = i % G::KF;
-        if (iF >= G::nF || n >= G::N1 || t0 + (n / G::nS) % G::TT >= T) Xs[n * G::PF + iF] = E(0.0f);
+    // While the loads fly: zero what no load writes. The contiguous-iF loader writes all of
+    // Xs; the scatter loader leaves the K padding, the rows iS >= nS and the rows of absent
+    // tokens (TT > 1) to this fill, which writes only those.
+    if constexpr (!G::XROW && (G::KF > G::nF || G::nSP > G::nS || G::TT > 1)) {
+        constexpr int CH = G::KF / 8;  // 16-byte chunks per row
+        for (int i = tid; i < G::N1 * CH; i += kThreads) {
+            const int n = i / CH, c = i % CH;
+            const bool empty_row = n % G::nSP >= G::nS || t0 + (n / G::nSP) % G::TT >= T;
+            if (empty_row || 8 * c >= G::nF) {
+                *reinterpret_cast<uint4 *>(Xs + n * G::PF + 8 * c) = make_uint4(0u, 0u, 0u, 0u);
+            } else if (G::nF % 8 != 0 && 8 * c + 8 > G::nF) {
+                for (int e = G::nF; e < 8 * c + 8; ++e) Xs[n * G::PF + e] = E(0.0f);
+            }
+        }
     }
     if constexpr (G::K2 > G::nS * R) {
         constexpr int pad = G::K2 - G::nS * R;
-        for (int i = tid; i < G::N2P * pad; i += kThreads)
+        for (int i = tid; i < G::N2R * pad; i += kThreads)
             Ub[(i / pad) * G::P2 + G::nS * R + i % pad] = E(0.0f);
     }
     commit_step(0);
@@ -506,6 +639,28 @@ __global__ void __launch_bounds__(kThreads)
         cS.commit(Ss);
     }
     __syncthreads();
+
+    // LDS store offsets of the stage-1 (Ub) and stage-2 (Vb) results, split into a part that
+    // depends on the tile only and a part that depends on the lane only.
+    //   Ub[(iL', r1, t, f)][(iS, r2)]:  stage-1 rows m = (f, r1, r2), columns n = (iL', t, iS)
+    //   Vb[(t, f, s)][(iL', r1, r3)]:   stage-2 rows m = (s, r3), columns n = (iL', r1, t, f)
+    auto ub_row = [](int m) { return ((m / R) % R * G::TT * G::FC + m / R2) * G::P2 + m % R; };
+    auto ub_col = [](int n) {
+        const int iS = n % G::nSP, t = (n / G::nSP) % G::TT, ilp = n / (G::nSP * G::TT);
+        return (ilp * R * G::TT * G::FC + t * G::FC) * G::P2 + iS * R;
+    };
+    auto vb_row = [](int m) { return (m / R) * G::P3 + m % R; };
+    auto vb_col = [](int n) {
+        constexpr int Q = G::FC * G::TT;  // (t, f) is n % Q, (iL', r1) is n / Q
+        return (n % Q) * G::SC * G::P3 + (n / Q) * R;
+    };
+    auto ub_tile = [&](int mt, int nt) { return ub_row(mt * 16) + ub_col(nt * 16); };
+    auto vb_tile = [&](int mt, int nt) { return vb_row(mt * 16) + vb_col(nt * 16); };
+    const int ub_lane = ub_row(4 * lgrp) + ub_col(lrow);
+    const int vb_lane = vb_row(4 * lgrp) + vb_col(lrow);
+    // 32x32 stage-2 tiles: rows mt*32 + 8*g + 4*(lane/32) + e, columns nt*32 + lane%32
+    auto vb_tile32 = [&](int mt, int nt) { return vb_row(mt * 32) + vb_col(nt * 32); };
+    const int vb_lane32 = vb_row(4 * (lane >> 5)) + vb_col(lane & 31);
 
     f32x4 acc[G::NYW][G::NACC];
 #pragma unroll
@@ -527,63 +682,63 @@ __global__ void __launch_bounds__(kThreads)
         // this step computes, so a step pays no memory latency of its own
         if (step + 1 < G::NSTEP) issue_step(iL0 + G::IC);
 
-        // stage 1: U^T = F . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]. The Ub offset of an entry is
-        // a row part (r1, f, r2) plus a column part (iL', t, iS).
-        auto ub_row = [&](int m0) {
-            return ((m0 / R) % R * G::TT * G::FC + m0 / R2) * G::P2 + m0 % R;
-        };
-        auto ub_col = [&](int n) {
-            const int iS = n % G::nS, t = (n / G::nS) % G::TT, ilp = n / (G::nS * G::TT);
-            return (ilp * R * G::TT * G::FC + t * G::FC) * G::P2 + iS * R;
-        };
+        // stage 1: U^T = F . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]. A tile (mt, nt) stores at
+        // ub_tile(mt, nt) + ub_lane: the rows (f, r1, r2) of mt*16 + 4*lgrp and the columns
+        // (iL', t, iS) of nt*16 + lrow split into tile and lane parts (R and 16 are powers of
+        // two and nSP is a multiple of 16, so no part carries into another).
         auto put4 = [&](E *dst, f32x4 d) {
             E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
             *reinterpret_cast<E4 *>(dst) = h;
         };
         if constexpr (G::WIDE) {
-            reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T>(fa, Xs, lrow, lgrp, [&](int nt, const f32x4 *d) {
-                const int n = nt * 16 + lrow;
-                if (G::N1 % 16 != 0 && n >= G::N1) return;
-                const int col = ub_col(n);
+            reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T, 1>(fa, Xs, 0, lrow, lgrp, [&](int nt, const f32x4 *d) {
+                if (G::nS % 16 != 0 && (nt % (G::nSP / 16)) * 16 + lrow >= G::nS) return;
 #pragma unroll
                 for (int i = 0; i < G::BM1; ++i) {
                     const int mt = wave * G::BM1 + i;
-                    if (G::M1T % 4 == 0 || mt < G::M1T) put4(Ub + col + ub_row(mt * 16 + 4 * lgrp), d[i]);
+                    if (G::M1T % 4 == 0 || mt < G::M1T) put4(Ub + ub_lane + ub_tile(mt, nt), d[i]);
                 }
             });
         } else {
             lds_gemm<O, G::M1T, G::N1T, G::KF, G::PF>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
-                const int n = nt * 16 + lrow;
-                if (G::N1 % 16 == 0 || n < G::N1) put4(Ub + ub_col(n) + ub_row(mt * 16 + 4 * lgrp), d);
+                if (G::nS % 16 == 0 || (nt % (G::nSP / 16)) * 16 + lrow < G::nS)
+                    put4(Ub + ub_lane + ub_tile(mt, nt), d);
             });
         }
         __syncthreads();
 
-        // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)]: row part (s, r3), column part
-        // (iL', r1, t, f)
-        auto vb_row = [&](int m0) { return (m0 / R) * G::P3 + m0 % R; };
-        auto vb_col = [&](int n) {
-            const int f = n % G::FC, t = (n / G::FC) % G::TT, r1 = (n / (G::FC * G::TT)) % R;
-            const int ilp = n / (G::FC * G::TT * R);
-            return (t * G::FC + f) * G::SC * G::P3 + (ilp * R + r1) * R;
-        };
-        if constexpr (G::WIDE) {
-            reg_gemm<O, G::BM2, G::K2, G::P2, G::N2T>(sa, Ub, lrow, lgrp, [&](int nt, const f32x4 *d) {
-                const int n = nt * 16 + lrow;
-                if (G::N2 % 16 != 0 && n >= G::N2) return;
-                const int col = vb_col(n);
+        // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)], rows (s, r3) of mt*16 + 4*lgrp
+        // and columns (iL', r1, t, f) of nt*16 + lrow split into tile and lane parts alike
+        if constexpr (G::W32) {
+            const int wm = wave % G::WM2, wn = wave / G::WM2;
+            reg_gemm32<O, G::BM2, G::K2, G::P2, G::N2T32, G::WN2>(sa, Ub, wn, lane, [&](int nt, const f32x16 *d) {
+                if (G::N2 % 32 != 0 && nt * 32 + (lane & 31) >= G::N2) return;
 #pragma unroll
                 for (int i = 0; i < G::BM2; ++i) {
-                    const int m0 = (wave * G::BM2 + i) * 16 + 4 * lgrp;
-                    if (G::M2 % 64 == 0 || m0 < G::M2) put4(Vb + col + vb_row(m0), d[i]);
+                    const int mt = wm * G::BM2 + i;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        if (G::M2 % (32 * G::WM2) == 0 || mt * 32 + 8 * g + 4 * (lane >> 5) < G::M2)
+                            put4(Vb + vb_lane32 + vb_tile32(mt, nt) + vb_row(8 * g),
+                                 f32x4{d[i][4 * g], d[i][4 * g + 1], d[i][4 * g + 2], d[i][4 * g + 3]});
+                }
+            });
+        } else if constexpr (G::WIDE) {
+            const int wm = wave % G::WM2, wn = wave / G::WM2;
+            reg_gemm<O, G::BM2, G::K2, G::P2, G::N2T, G::WN2>(sa, Ub, wn, lrow, lgrp, [&](int nt, const f32x4 *d) {
+                if (G::N2 % 16 != 0 && nt * 16 + lrow >= G::N2) return;
+#pragma unroll
+                for (int i = 0; i < G::BM2; ++i) {
+                    const int mt = wm * G::BM2 + i;
+                    if (G::M2 % (16 * G::WM2) == 0 || mt * 16 + 4 * lgrp < G::M2)
+                        put4(Vb + vb_lane + vb_tile(mt, nt), d[i]);
                 }
             });
         } else {
             lds_gemm<O, G::M2T, G::N2T, G::K2, G::P2>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
-                const int n = nt * 16 + lrow;
-                const int m0 = mt * 16 + 4 * lgrp;
-                if ((G::N2 % 16 == 0 || n < G::N2) && (G::M2 % 16 == 0 || m0 < G::M2))
-                    put4(Vb + vb_col(n) + vb_row(m0), d);
+                if ((G::N2 % 16 == 0 || nt * 16 + lrow < G::N2) &&
+                    (G::M2 % 16 == 0 || mt * 16 + 4 * lgrp < G::M2))
+                    put4(Vb + vb_lane + vb_tile(mt, nt), d);
             });
         }
         __syncthreads();
@@ -687,65 +842,78 @@ struct Entry {
     LaunchFn launch;
 };
 
-#define TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W) \
-    KCfg { DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W }
-#define TRK_ENTRY(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W,      \
-                  TMIN, TMAX)                                                                    \
-    {TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC, W), TMIN,     \
-     TMAX,                                                                                       \
-     Geo<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC,          \
-                 W)>::LDS_BYTES,                                                                  \
-     launch_mfma<TRK_CFG(DT, F, S, L, I0, I1, I2, O0, O1, O2, R, TT, FC, SC, LC, IC, KS3, NACC,   \
-                         W)>},
+// One shape of the variant table (dtype, chain order, modes, rank); tile() completes it.
+struct Shape {
+    int dt, F, S, L, i0, i1, i2, o0, o1, o2, R;
+};
+constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
+                    int WIDE = 0, int MF2 = 16) {
+    return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2};
+}
+constexpr Shape kR8{TRK_DTYPE_F16, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8};
+constexpr Shape kR16{TRK_DTYPE_F16, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16};
+constexpr Shape kUp{TRK_DTYPE_BF16, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8};
+constexpr Shape kDown{TRK_DTYPE_BF16, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16};
 
-constexpr int H = TRK_DTYPE_F16, B = TRK_DTYPE_BF16;
+#define TRK_ENTRY(CFG, TMIN, TMAX) {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>},
 
-// dtype, order F S L, input modes, output modes, rank, tile TT FC SC LC IC, stage-3 KS3 NACC,
-// WIDE, default token range (0 0: reachable by index only)
+// tile(shape, TT, FC, SC, LC, IC, stage-3 KS3, NACC[, WIDE (the waves splitting the stage-2
+// rows), stage-2 MFMA edge]), default token range (0 0: reachable by index only)
 const Entry kEntries[] = {
-    // 1920 -> 2880, (8,12,20) -> (12,10,24), rank 8, fp16
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 1, 4, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 4, 1, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 4, 1, 1, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 2, 12, 8, 2, 2, 0, 1, 1)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 1, 12, 8, 1, 4, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 5, 12, 8, 1, 4, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 2, 5, 12, 8, 1, 4, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 4, 1, 10, 12, 4, 2, 1, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 1, 1, 10, 12, 8, 1, 4, 1, 2, 1 << 30)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8, 4, 1, 10, 12, 4, 2, 1, 1, 0, 0)
+    // 1920 -> 2880, (8,12,20) -> (12,10,24), rank 8, fp16, chain (G3, G2, G1)
+    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 4, 1), 1, 1)
+    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 4, 1, 1), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 2, 2), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 1, 12, 8, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 5, 12, 8, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 10, 12, 8, 1, 4), 2, 1 << 30)
+    TRK_ENTRY(tile(kR8, 1, 2, 5, 12, 8, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kR8, 4, 1, 10, 12, 4, 2, 1), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 10, 12, 8, 1, 4, 1), 0, 0)
+    TRK_ENTRY(tile(kR8, 4, 1, 10, 12, 4, 2, 1, 1), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 10, 12, 8, 1, 4, 2, 32), 0, 0)
+    TRK_ENTRY(tile(kR8, 4, 1, 10, 12, 4, 2, 1, 1, 32), 0, 0)
     // same modes, rank 16, fp16
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 2, 2, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 4, 1, 0, 1, 1)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 1, 12, 4, 4, 1, 1, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 2, 12, 4, 4, 1, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 5, 12, 4, 1, 4, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 5, 12, 2, 2, 1, 0, 0, 0)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 1, 1, 10, 12, 2, 1, 4, 1, 2, 24)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 4, 1, 10, 12, 2, 2, 1, 1, 25, 1 << 30)
-    TRK_ENTRY(H, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16, 2, 1, 10, 12, 4, 1, 4, 1, 0, 0)
-    // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 2, 2, 0, 1, 1)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 4, 1, 0, 0, 0)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 2, 32, 8, 4, 1, 1, 0, 0)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 4, 32, 8, 2, 2, 0, 0, 0)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 7, 32, 8, 1, 2, 0, 0, 0)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 14, 32, 8, 1, 2, 0, 2, 8)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 28, 32, 8, 1, 2, 0, 9, 64)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 1, 1, 28, 32, 8, 1, 2, 1, 0, 0)
-    TRK_ENTRY(B, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8, 4, 1, 28, 32, 4, 1, 2, 1, 65, 1 << 30)
-    // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 0, 1, 1)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 1, 16, 2, 4, 1, 1, 0, 0)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 1, 1, 2, 16, 2, 4, 1, 0, 0, 0)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 4, 16, 1, 2, 1, 0, 0, 0)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 8, 16, 1, 2, 1, 1, 2, 128)
-    TRK_ENTRY(B, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16, 4, 1, 16, 16, 1, 2, 1, 1, 129, 1 << 30)
+    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 2, 2), 0, 0)
+    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 4, 1), 1, 1)
+    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 4, 1, 1), 0, 0)
+    TRK_ENTRY(tile(kR16, 1, 1, 2, 12, 4, 4, 1), 0, 0)
+    TRK_ENTRY(tile(kR16, 1, 1, 5, 12, 4, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4, 2), 0, 0)
+    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 2), 25, 1 << 30)
+    TRK_ENTRY(tile(kR16, 2, 1, 10, 12, 4, 1, 4, 2), 0, 0)
+    TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4, 4, 32), 2, 24)
+    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 2, 32), 0, 0)
+    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 4, 32), 0, 0)
+    TRK_ENTRY(tile(kR16, 2, 1, 10, 12, 4, 1, 4, 4, 32), 0, 0)
+    // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16, chain (G1, G2, G3)
+    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 2, 2), 1, 1)
+    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 4, 1), 0, 0)
+    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 4, 1, 1), 0, 0)
+    TRK_ENTRY(tile(kUp, 1, 1, 4, 32, 8, 2, 2), 0, 0)
+    TRK_ENTRY(tile(kUp, 1, 1, 7, 32, 8, 1, 2), 0, 0)
+    TRK_ENTRY(tile(kUp, 1, 1, 14, 32, 8, 1, 2), 2, 8)
+    TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2), 9, 64)
+    TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2, 2), 0, 0)
+    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 2), 0, 0)
+    TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2, 2, 32), 0, 0)
+    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 2, 32), 0, 0)
+    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 4, 32), 65, 1 << 30)
+    // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16, chain (G3, G2, G1)
+    TRK_ENTRY(tile(kDown, 1, 1, 1, 16, 2, 4, 1), 1, 1)
+    TRK_ENTRY(tile(kDown, 1, 1, 1, 16, 2, 4, 1, 1), 0, 0)
+    TRK_ENTRY(tile(kDown, 1, 1, 2, 16, 2, 4, 1), 0, 0)
+    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 2), 0, 0)
+    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 4), 0, 0)
+    TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 4, 32), 129, 1 << 30)
+    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 4, 32), 2, 128)
+    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 2, 32), 0, 0)
 };
 #undef TRK_ENTRY
-#undef TRK_CFG
 
 }  // namespace
 
@@ -774,9 +942,13 @@ int mfma_register(Plan *plan) {
         v.t_min = e.t_min;
         v.t_max = e.t_max;
         v.launch = e.launch;
-        std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
-                      k.WIDE ? "_wide" : "", k.F, k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3,
-                      k.NACC);
+        if (k.WIDE)
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma_wide%d%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+                          k.WIDE, k.MF2 == 32 ? "x32" : "", k.F, k.S, k.L, k.TT, k.FC, k.SC, k.LC,
+                          k.IC, k.KS3, k.NACC);
+        else
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.F,
+                          k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         ++added;
     }
     return added;

@@ -26,9 +26,11 @@ ARCH = "gfx950"
 # -packed-fp32-ops: no packed fp32 VALU ops (v_pk_*_f32) anywhere in the device code.
 # -amdgpu-kernarg-preload-count: kernel arguments arrive in SGPRs at wave start instead of
 # being fetched from memory first (a memory latency off the front of every launch).
+# -amdgpu-mfma-vgpr-form: MFMA results go to ordinary VGPRs, so the epilogues that convert
+# and store them need no accumulator-register reads.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",
-    "-mllvm", "-amdgpu-kernarg-preload-count=16",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
