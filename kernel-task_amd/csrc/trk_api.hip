@@ -162,7 +162,8 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     g.t_min = 1;
     g.t_max = 1 << 30;
     p->nvariants = 1;
-    mfma_register(p);
+    mfma_register_lds(p);
+    mfma_register_wide(p);
     *out = reinterpret_cast<trk_plan *>(p);
     return TRK_OK;
 }

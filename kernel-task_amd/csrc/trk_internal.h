@@ -78,8 +78,9 @@ int launch_generic(const Plan &plan, const Variant &v, const void *packed, const
                    void *y, int tokens, hipStream_t stream);           // trk_generic.hip
 int launch_empty(hipStream_t stream);                                  // trk_generic.hip
 
-// MFMA variants compiled for this plan's shape (trk_mfma.hip): appends to plan->variants
-// and returns how many were added.
-int mfma_register(Plan *plan);
+// MFMA variants compiled for this plan's shape: appends to plan->variants and returns how
+// many were added (trk_mfma_lds.hip: core slices in LDS; trk_mfma_wide.hip: in registers).
+int mfma_register_lds(Plan *plan);
+int mfma_register_wide(Plan *plan);
 
 }  // namespace trk

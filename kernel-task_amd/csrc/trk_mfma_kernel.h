@@ -1,4 +1,8 @@
-// MFMA (gfx950 matrix core) variants of the fused tensor-ring kernel, fp16 and bf16.
+#pragma once
+// MFMA (gfx950 matrix core) variants of the fused tensor-ring kernel, fp16 and bf16: the
+// kernel template, its launch and the variant-table helpers. The tables themselves live in
+// trk_mfma_lds.hip (core slices in LDS) and trk_mfma_wide.hip (core slices in registers),
+// two translation units so that each family gets its own compiler flags.
 //
 // Role of the reference's V3 / V3T / V3G kernels (tr_ring.cu:543-751, :822-1056,
 // csrc/v3g/v3g.cuh:142-431); own design for CDNA4:
@@ -858,68 +862,11 @@ constexpr Shape kDown{TRK_DTYPE_BF16, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16};
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>},
 
-// tile(shape, TT, FC, SC, LC, IC, stage-3 KS3, NACC[, WIDE (the waves splitting the stage-2
-// rows), stage-2 MFMA edge]), default token range (0 0: reachable by index only)
-const Entry kEntries[] = {
-    // 1920 -> 2880, (8,12,20) -> (12,10,24), rank 8, fp16, chain (G3, G2, G1)
-    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 4, 1), 1, 1)
-    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 4, 1, 1), 0, 0)
-    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 2, 2), 0, 0)
-    TRK_ENTRY(tile(kR8, 1, 1, 1, 12, 8, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kR8, 1, 1, 5, 12, 8, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kR8, 1, 1, 10, 12, 8, 1, 4), 2, 1 << 30)
-    TRK_ENTRY(tile(kR8, 1, 2, 5, 12, 8, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kR8, 4, 1, 10, 12, 4, 2, 1), 0, 0)
-    TRK_ENTRY(tile(kR8, 1, 1, 10, 12, 8, 1, 4, 1), 0, 0)
-    TRK_ENTRY(tile(kR8, 4, 1, 10, 12, 4, 2, 1, 1), 0, 0)
-    TRK_ENTRY(tile(kR8, 1, 1, 10, 12, 8, 1, 4, 2, 32), 0, 0)
-    TRK_ENTRY(tile(kR8, 4, 1, 10, 12, 4, 2, 1, 1, 32), 0, 0)
-    // same modes, rank 16, fp16
-    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 2, 2), 0, 0)
-    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 4, 1), 1, 1)
-    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 4, 1, 1), 0, 0)
-    TRK_ENTRY(tile(kR16, 1, 1, 2, 12, 4, 4, 1), 0, 0)
-    TRK_ENTRY(tile(kR16, 1, 1, 5, 12, 4, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4, 2), 0, 0)
-    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 2), 25, 1 << 30)
-    TRK_ENTRY(tile(kR16, 2, 1, 10, 12, 4, 1, 4, 2), 0, 0)
-    TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4, 4, 32), 2, 24)
-    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 2, 32), 0, 0)
-    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 4, 32), 0, 0)
-    TRK_ENTRY(tile(kR16, 2, 1, 10, 12, 4, 1, 4, 4, 32), 0, 0)
-    // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16, chain (G1, G2, G3)
-    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 2, 2), 1, 1)
-    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 4, 1), 0, 0)
-    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 4, 1, 1), 0, 0)
-    TRK_ENTRY(tile(kUp, 1, 1, 4, 32, 8, 2, 2), 0, 0)
-    TRK_ENTRY(tile(kUp, 1, 1, 7, 32, 8, 1, 2), 0, 0)
-    TRK_ENTRY(tile(kUp, 1, 1, 14, 32, 8, 1, 2), 2, 8)
-    TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2), 9, 64)
-    TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2, 2), 0, 0)
-    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 2), 0, 0)
-    TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2, 2, 32), 0, 0)
-    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 2, 32), 0, 0)
-    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 4, 32), 65, 1 << 30)
-    // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16, chain (G3, G2, G1)
-    TRK_ENTRY(tile(kDown, 1, 1, 1, 16, 2, 4, 1), 1, 1)
-    TRK_ENTRY(tile(kDown, 1, 1, 1, 16, 2, 4, 1, 1), 0, 0)
-    TRK_ENTRY(tile(kDown, 1, 1, 2, 16, 2, 4, 1), 0, 0)
-    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 2), 0, 0)
-    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 4, 32), 129, 1 << 30)
-    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 4, 32), 2, 128)
-    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 2, 32), 0, 0)
-};
-#undef TRK_ENTRY
-
-}  // namespace
-
-int mfma_register(Plan *plan) {
+// Appends the variants of `entries` that match the plan's shape and dtype; returns how many.
+inline int register_entries(Plan *plan, const Entry *entries, int count) {
     int added = 0;
-    for (const Entry &e : kEntries) {
+    for (const Entry *p = entries; p != entries + count; ++p) {
+        const Entry &e = *p;
         const KCfg &k = e.cfg;
         const int ins[3] = {k.i0, k.i1, k.i2}, outs[3] = {k.o0, k.o1, k.o2};
         if (k.dt != plan->dtype || k.R != plan->rank || !std::equal(ins, ins + 3, plan->in_modes) ||
@@ -954,4 +901,5 @@ int mfma_register(Plan *plan) {
     return added;
 }
 
+}  // namespace
 }  // namespace trk
