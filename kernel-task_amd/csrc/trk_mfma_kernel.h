@@ -96,6 +96,7 @@ struct KCfg {
                              // rows while 4 / WIDE waves split its columns
     int MF2;                 // WIDE stage-2 MFMA: 16 (16x16x32) or 32 (32x32x16, twice the
                              // matrix-core throughput of 16x16x32 on gfx950)
+    int NW;                  // waves per workgroup: 4 (one per SIMD) or 8 (two per SIMD)
 };
 
 template <KCfg C>
@@ -131,7 +132,8 @@ struct Geo {
     static constexpr int M3 = TT * FC * SC, M3T = cdiv(M3, 16), M3P = M3T * 16;
     static constexpr int N3T = cdiv(LC, 16), LCP = N3T * 16;
     static constexpr int K3 = IC * R2;
-    static constexpr int NT3 = M3T * N3T, G3 = 4 / KS3, NYW = cdiv(NT3, G3);
+    static constexpr int NW = C.NW, NT = 64 * NW;  // waves and threads per workgroup
+    static constexpr int NT3 = M3T * N3T, G3 = NW / KS3, NYW = cdiv(NT3, G3);
     static constexpr int NSTEP = cdiv(nL, IC);
     static constexpr int NFC = cdiv(oF, FC), NSC = cdiv(oS, SC), NLC = cdiv(oL, LC);
     static constexpr int NBLK = NFC * NSC * NLC;  // workgroups per token tile
@@ -143,10 +145,10 @@ struct Geo {
     static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * P2;
     // WIDE: each wave holds the A fragments of BM1 stage-1 and BM2 stage-2 row tiles; stage 2
     // runs on a WM2 x WN2 grid of waves (rows x columns)
-    static constexpr int WM2 = WIDE ? C.WIDE : 4, WN2 = 4 / WM2;
+    static constexpr int WM2 = WIDE ? C.WIDE : NW, WN2 = NW / WM2;
     static constexpr bool W32 = WIDE && C.MF2 == 32;  // stage 2 on 32x32 tiles
     static constexpr int M2T32 = cdiv(M2, 32), N2T32 = cdiv(N2, 32);
-    static constexpr int BM1 = cdiv(M1T, 4), BM2 = cdiv(W32 ? M2T32 : M2T, WM2);
+    static constexpr int BM1 = cdiv(M1T, NW), BM2 = cdiv(W32 ? M2T32 : M2T, WM2);
     static constexpr int N2R = W32 ? N2T32 * 32 : N2P;  // Ub rows (the last tile's padding)
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
     static constexpr int oXs = oLs + szLs, szXs = N1P * PF;
@@ -168,10 +170,12 @@ struct Geo {
     static constexpr int XB = 8;
 
     static_assert(R % 8 == 0 && (R & (R - 1)) == 0, "MFMA variants need a power-of-two rank >= 8");
-    static_assert(C.WIDE == 0 || C.WIDE == 1 || C.WIDE == 2 || C.WIDE == 4, "WIDE is 0, 1, 2 or 4");
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
+    static_assert(C.WIDE >= 0 && C.WIDE <= NW && (C.WIDE == 0 || NW % C.WIDE == 0),
+                  "WIDE is 0 or divides the waves");
     static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
     static_assert(16 % (FC * TT) == 0, "FC * TT must divide 16 (stage-2 store offsets)");
-    static_assert(KS3 == 1 || KS3 == 2 || KS3 == 4, "KS3 must divide the 4 waves");
+    static_assert(KS3 >= 1 && NW % KS3 == 0, "KS3 must divide the waves");
     static_assert(NACC >= 1 && (K3 / 32 / KS3) % NACC == 0, "NACC must divide a wave's K steps");
     static_assert(FC <= oF && SC <= oS && LC <= oL && IC <= nL && TT >= 1, "tile too large");
     static_assert(LDS_BYTES <= 160 * 1024, "workgroup tile exceeds the 160 KB of LDS");
@@ -180,35 +184,35 @@ struct Geo {
     static_assert(XROW || IN % 8 == 0, "scatter loader reads x rows in 8-element vectors");
 };
 
-constexpr int kThreads = 256;
 
 // Wait for every outstanding global load of this wave.
 __device__ inline void wait_loads() { __builtin_amdgcn_s_waitcnt(0); }
 
-// LDS <- global through VGPRs for NB blocks of BLOCK 16-byte vectors: block b is read from
-// src + b * stride (vectors), its first `valid` vectors from memory and the rest zero.
-// issue() starts every read of the copy; commit(), after wait_loads(), writes the LDS as
-// rows of ROW vectors, each followed by one vector of pitch padding.
-template <int NB, int BLOCK, int ROW>
+// LDS <- global through VGPRs for NB blocks of BLOCK 16-byte vectors, spread over the NT
+// threads of a workgroup: block b is read from src + b * stride (vectors), its first `valid`
+// vectors from memory and the rest zero. issue() starts every read of the copy; commit(),
+// after wait_loads(), writes the LDS as rows of ROW vectors, each followed by one vector of
+// pitch padding.
+template <int NB, int BLOCK, int ROW, int NT>
 struct RegCopy {
     static_assert(BLOCK % ROW == 0, "a copy block holds whole LDS rows");
-    static constexpr int TOTAL = NB * BLOCK, PER = cdiv(TOTAL, kThreads);
+    static constexpr int TOTAL = NB * BLOCK, PER = cdiv(TOTAL, NT);
     uint4 r[PER];
     __device__ __forceinline__ void issue(const void *src, size_t stride, int valid) {
         const uint4 *s = static_cast<const uint4 *>(src);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
-            const int i = threadIdx.x + j * kThreads, b = i / BLOCK, w = i % BLOCK;
+            const int i = threadIdx.x + j * NT, b = i / BLOCK, w = i % BLOCK;
             r[j] = make_uint4(0u, 0u, 0u, 0u);
-            if ((TOTAL % kThreads == 0 || i < TOTAL) && w < valid) r[j] = s[b * stride + w];
+            if ((TOTAL % NT == 0 || i < TOTAL) && w < valid) r[j] = s[b * stride + w];
         }
     }
     __device__ __forceinline__ void commit(void *dst) const {
         uint4 *d = static_cast<uint4 *>(dst);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
-            const int i = threadIdx.x + j * kThreads;
-            if (TOTAL % kThreads == 0 || i < TOTAL) d[i + i / ROW] = r[j];
+            const int i = threadIdx.x + j * NT;
+            if (TOTAL % NT == 0 || i < TOTAL) d[i + i / ROW] = r[j];
         }
     }
 };
@@ -232,14 +236,14 @@ struct VecOf<2> { using T = unsigned short; };
 struct Blocking {
     int bm, bn;
 };
-constexpr Blocking choose_blocking(int MT, int NT, int KS) {
+constexpr Blocking choose_blocking(int MT, int NT, int KS, int NW) {
     Blocking best{1, 1};
     long best_cost = -1;
     for (int bm = 1; bm <= 4; ++bm)
         for (int bn = 1; bn <= 8; ++bn) {
             if (bm * bn > 16 || bm > MT || bn > NT) continue;
             const int blocks = cdiv(MT, bm) * cdiv(NT, bn);
-            const long per_wave = cdiv(blocks, 4);
+            const long per_wave = cdiv(blocks, NW);
             const long cost = per_wave * KS * (16L * bm * bn + 12L * (bm + bn)) + per_wave * 40;
             if (best_cost < 0 || cost < best_cost) {
                 best_cost = cost;
@@ -251,19 +255,19 @@ constexpr Blocking choose_blocking(int MT, int NT, int KS) {
 
 // One LDS GEMM stage: D[MT*16][NT*16] = A[.][K] . B[.][K]^T (rows K-contiguous, pitch P),
 // register-blocked as above; each finished tile goes to st(mt, nt, d).
-template <class O, int MT, int NT, int K, int P, class Store>
+template <class O, int MT, int NT, int K, int P, int NW, class Store>
 __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename O::E *B, int wave,
                                          int lrow, int lgrp, Store &&st) {
     using V8 = typename O::V8;
     using V4 = typename O::V4;
     constexpr int K32 = K / 32, K16 = (K % 32) / 16;
-    constexpr Blocking BK = choose_blocking(MT, NT, K32 + K16);
+    constexpr Blocking BK = choose_blocking(MT, NT, K32 + K16, NW);
     constexpr int BM = BK.bm, BN = BK.bn, NBM = cdiv(MT, BM), NBN = cdiv(NT, BN);
     constexpr int BLOCKS = NBM * NBN;
 #pragma unroll
-    for (int j = 0; j < cdiv(BLOCKS, 4); ++j) {
-        const int blk = wave + 4 * j;
-        if (BLOCKS % 4 != 0 && blk >= BLOCKS) break;
+    for (int j = 0; j < cdiv(BLOCKS, NW); ++j) {
+        const int blk = wave + NW * j;
+        if (BLOCKS % NW != 0 && blk >= BLOCKS) break;
         const int m0 = (blk / NBN) * BM, n0 = (blk % NBN) * BN;
         const typename O::E *a = A + (m0 * 16 + lrow) * P;
         const typename O::E *b = B + (n0 * 16 + lrow) * P;
@@ -486,7 +490,7 @@ __device__ __forceinline__ void reg_gemm32(const RegA32<O, BMW, K> &A, const typ
 }
 
 template <KCfg C>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(Geo<C>::NT)
     ring3_mfma_kernel(const typename Ops<C.dt>::E *__restrict__ x,
                       const typename Ops<C.dt>::E *__restrict__ Fk,
                       const typename Ops<C.dt>::E *__restrict__ Sk,
@@ -527,7 +531,7 @@ __global__ void __launch_bounds__(kThreads)
     // read into registers (issue), then written to Ls and Xs[(iL', t, iS)][iF] (commit).
     // Every global read of a step is in flight before the first wait.
     using XV = typename VecOf<2 * G::VX>::T;
-    constexpr int XPER = G::XROW ? cdiv(G::NXV, kThreads) : cdiv(G::NXB, kThreads);
+    constexpr int XPER = G::XROW ? cdiv(G::NXV, G::NT) : cdiv(G::NXB, G::NT);
     constexpr int XREG = G::XROW ? XPER : (XPER < G::XB ? XPER : G::XB);
     XV xr[G::XROW ? XREG : 1];
     uint4 xb[G::XROW ? 1 : XREG];
@@ -538,7 +542,7 @@ __global__ void __launch_bounds__(kThreads)
         const int n = v / G::XCPR, c = v % G::XCPR;
         const int iS = n % G::nSP, t = (n / G::nSP) % G::TT, iL = iL0 + n / (G::nSP * G::TT);
         XV r{};
-        if ((G::NXV % kThreads == 0 || v < G::NXV) && c * G::VX < G::nF && iS < G::nS &&
+        if ((G::NXV % G::NT == 0 || v < G::NXV) && c * G::VX < G::nF && iS < G::nS &&
             t0 + t < T)
             r = *reinterpret_cast<const XV *>(x + size_t(t0 + t) * G::IN + iS * G::SXS +
                                               iL * G::SXL + c * G::VX);
@@ -563,17 +567,17 @@ __global__ void __launch_bounds__(kThreads)
             if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nSP + iS) * G::PF + iF] = e[q];
         }
     };
-    RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8> cF;
-    RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8> cS;
-    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8> cL;
+    RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT> cF;
+    RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8, G::NT> cS;
+    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, G::NT> cL;
     auto issue_step = [&](int iL0) {
         cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
         if constexpr (G::XROW) {
 #pragma unroll
-            for (int j = 0; j < XREG; ++j) xr[j] = x_row_load(tid + j * kThreads, iL0);
+            for (int j = 0; j < XREG; ++j) xr[j] = x_row_load(tid + j * G::NT, iL0);
         } else {
 #pragma unroll
-            for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * kThreads);
+            for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * G::NT);
         }
     };
     auto commit_step = [&](int iL0) {
@@ -582,23 +586,23 @@ __global__ void __launch_bounds__(kThreads)
         if constexpr (G::XROW) {
 #pragma unroll
             for (int j = 0; j < XREG; ++j) {
-                const int v = tid + j * kThreads;
-                if (G::NXV % kThreads == 0 || v < G::NXV)
+                const int v = tid + j * G::NT;
+                if (G::NXV % G::NT == 0 || v < G::NXV)
                     *reinterpret_cast<XV *>(Xs + (v / G::XCPR) * G::PF + (v % G::XCPR) * G::VX) =
                         xr[j];
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < XREG; ++j) x_scatter_store(tid + j * kThreads, xb[j], iL0);
+            for (int j = 0; j < XREG; ++j) x_scatter_store(tid + j * G::NT, xb[j], iL0);
             for (int j0 = XREG; j0 < XPER; j0 += XREG) {  // further batches, one latency each
 #pragma unroll
                 for (int j = 0; j < XREG; ++j)
-                    xb[j] = j0 + j < XPER ? x_scatter_load(tid + (j0 + j) * kThreads)
+                    xb[j] = j0 + j < XPER ? x_scatter_load(tid + (j0 + j) * G::NT)
                                           : make_uint4(0u, 0u, 0u, 0u);
                 wait_loads();
 #pragma unroll
                 for (int j = 0; j < XREG; ++j)
-                    if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * kThreads, xb[j], iL0);
+                    if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * G::NT, xb[j], iL0);
             }
         }
     };
@@ -622,7 +626,7 @@ __global__ void __launch_bounds__(kThreads)
     // tokens (TT > 1) to this fill, which writes only those.
     if constexpr (!G::XROW && (G::KF > G::nF || G::nSP > G::nS || G::TT > 1)) {
         constexpr int CH = G::KF / 8;  // 16-byte chunks per row
-        for (int i = tid; i < G::N1 * CH; i += kThreads) {
+        for (int i = tid; i < G::N1 * CH; i += G::NT) {
             const int n = i / CH, c = i % CH;
             const bool empty_row = n % G::nSP >= G::nS || t0 + (n / G::nSP) % G::TT >= T;
             if (empty_row || 8 * c >= G::nF) {
@@ -634,7 +638,7 @@ __global__ void __launch_bounds__(kThreads)
     }
     if constexpr (G::K2 > G::nS * R) {
         constexpr int pad = G::K2 - G::nS * R;
-        for (int i = tid; i < G::N2R * pad; i += kThreads)
+        for (int i = tid; i < G::N2R * pad; i += G::NT)
             Ub[(i / pad) * G::P2 + G::nS * R + i % pad] = E(0.0f);
     }
     commit_step(0);
@@ -700,11 +704,11 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
                 for (int i = 0; i < G::BM1; ++i) {
                     const int mt = wave * G::BM1 + i;
-                    if (G::M1T % 4 == 0 || mt < G::M1T) put4(Ub + ub_lane + ub_tile(mt, nt), d[i]);
+                    if (G::M1T % G::NW == 0 || mt < G::M1T) put4(Ub + ub_lane + ub_tile(mt, nt), d[i]);
                 }
             });
         } else {
-            lds_gemm<O, G::M1T, G::N1T, G::KF, G::PF>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            lds_gemm<O, G::M1T, G::N1T, G::KF, G::PF, G::NW>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
                 if (G::nS % 16 == 0 || (nt % (G::nSP / 16)) * 16 + lrow < G::nS)
                     put4(Ub + ub_lane + ub_tile(mt, nt), d);
             });
@@ -739,7 +743,7 @@ __global__ void __launch_bounds__(kThreads)
                 }
             });
         } else {
-            lds_gemm<O, G::M2T, G::N2T, G::K2, G::P2>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            lds_gemm<O, G::M2T, G::N2T, G::K2, G::P2, G::NW>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
                 if ((G::N2 % 16 == 0 || nt * 16 + lrow < G::N2) &&
                     (G::M2 % 16 == 0 || mt * 16 + 4 * lgrp < G::M2))
                     put4(Vb + vb_lane + vb_tile(mt, nt), d);
@@ -832,7 +836,7 @@ int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const vo
     if (grid.y > 65535u)
         return set_error(TRK_ERR_UNSUPPORTED, "trk_forward: %d tokens exceed one launch of %s",
                          tokens, v.name);
-    hipLaunchKernelGGL(ring3_mfma_kernel<C>, grid, dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL(ring3_mfma_kernel<C>, grid, dim3(G::NT), 0, stream,
                        static_cast<const E *>(x), reinterpret_cast<const E *>(base + c.offF),
                        reinterpret_cast<const E *>(base + c.offS),
                        reinterpret_cast<const E *>(base + c.offL), static_cast<E *>(y), tokens);
@@ -851,9 +855,9 @@ struct Shape {
     int dt, F, S, L, i0, i1, i2, o0, o1, o2, R;
 };
 constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
-                    int WIDE = 0, int MF2 = 16) {
+                    int WIDE = 0, int MF2 = 16, int NW = 4) {
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
-                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2};
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW};
 }
 constexpr Shape kR8{TRK_DTYPE_F16, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8};
 constexpr Shape kR16{TRK_DTYPE_F16, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16};
@@ -884,15 +888,15 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
         v.tile[2] = k.SC;
         v.tile[3] = k.LC;
         v.tile[4] = k.IC;
-        v.block = kThreads;
+        v.block = 64 * k.NW;
         v.lds_bytes = e.lds_bytes;
         v.t_min = e.t_min;
         v.t_max = e.t_max;
         v.launch = e.launch;
         if (k.WIDE)
-            std::snprintf(v.name, sizeof(v.name), "ring3_mfma_wide%d%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
-                          k.WIDE, k.MF2 == 32 ? "x32" : "", k.F, k.S, k.L, k.TT, k.FC, k.SC, k.LC,
-                          k.IC, k.KS3, k.NACC);
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma_wide%d%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+                          k.WIDE, k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "", k.F, k.S, k.L,
+                          k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         else
             std::snprintf(v.name, sizeof(v.name), "ring3_mfma<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);

@@ -17,27 +17,34 @@ const Entry kEntries[] = {
     // same modes, rank 16, fp16
     TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 4, 1, 1), 0, 0)
     TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4, 2), 0, 0)
-    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 2), 25, 1 << 30)
+    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 2), 0, 0)
     TRK_ENTRY(tile(kR16, 2, 1, 10, 12, 4, 1, 4, 2), 0, 0)
     TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4, 4, 32), 2, 24)
     TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 2, 32), 0, 0)
     TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 4, 32), 0, 0)
     TRK_ENTRY(tile(kR16, 2, 1, 10, 12, 4, 1, 4, 4, 32), 0, 0)
+    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 4, 32, 8), 0, 0)
+    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 2, 1, 8, 32, 8), 25, 1 << 30)
+    TRK_ENTRY(tile(kR16, 4, 1, 10, 12, 2, 4, 1, 2, 16, 8), 0, 0)
     // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16, chain (G1, G2, G3)
     TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 4, 1, 1), 0, 0)
     TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2, 2), 0, 0)
     TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 2), 0, 0)
     TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2, 2, 32), 0, 0)
     TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 2, 32), 0, 0)
-    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 4, 32), 65, 1 << 30)
+    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 4, 32), 0, 0)
+    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 8, 32, 8), 65, 1 << 30)
+    TRK_ENTRY(tile(kUp, 4, 1, 28, 32, 4, 1, 2, 4, 32, 8), 0, 0)
     // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16, chain (G3, G2, G1)
     TRK_ENTRY(tile(kDown, 1, 1, 1, 16, 2, 4, 1, 1), 0, 0)
     TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 2), 0, 0)
     TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 4), 0, 0)
     TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 4), 0, 0)
-    TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 4, 32), 129, 1 << 30)
+    TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 4, 32), 0, 0)
     TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 4, 32), 2, 128)
     TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 2, 32), 0, 0)
+    TRK_ENTRY(tile(kDown, 4, 1, 16, 16, 1, 2, 1, 8, 32, 8), 129, 1 << 30)
+    TRK_ENTRY(tile(kDown, 4, 1, 8, 16, 1, 2, 1, 4, 32, 8), 0, 0)
 };
 
 }  // namespace
