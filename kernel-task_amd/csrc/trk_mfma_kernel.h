@@ -898,8 +898,9 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
                           k.WIDE, k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "", k.F, k.S, k.L,
                           k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         else
-            std::snprintf(v.name, sizeof(v.name), "ring3_mfma<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.F,
-                          k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+                          k.NW == 8 ? "_w8" : "", k.F, k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC,
+                          k.KS3, k.NACC);
         ++added;
     }
     return added;

@@ -11,6 +11,10 @@ const Entry kEntries[] = {
     // 1920 -> 2880, (8,12,20) -> (12,10,24), rank 8, fp16, chain (G3, G2, G1)
     TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 1, 4), 0, 0)
     TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 4, 1), 1, 1)
+    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 8, 1, 0, 16, 8), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 4, 1, 0, 16, 8), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 1, 12, 8, 8, 1, 0, 16, 8), 0, 0)
+    TRK_ENTRY(tile(kR8, 1, 1, 4, 12, 8, 8, 1, 0, 16, 8), 0, 0)
     TRK_ENTRY(tile(kR8, 1, 1, 2, 12, 8, 2, 2), 0, 0)
     TRK_ENTRY(tile(kR8, 1, 1, 1, 12, 8, 1, 4), 0, 0)
     TRK_ENTRY(tile(kR8, 1, 1, 5, 12, 8, 1, 4), 0, 0)
@@ -19,12 +23,15 @@ const Entry kEntries[] = {
     TRK_ENTRY(tile(kR8, 4, 1, 10, 12, 4, 2, 1), 0, 0)
     // same modes, rank 16, fp16
     TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 2, 2), 0, 0)
-    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 4, 1), 1, 1)
+    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 4, 1), 0, 0)
+    TRK_ENTRY(tile(kR16, 1, 1, 1, 12, 4, 8, 1, 0, 16, 8), 1, 1)
     TRK_ENTRY(tile(kR16, 1, 1, 2, 12, 4, 4, 1), 0, 0)
     TRK_ENTRY(tile(kR16, 1, 1, 5, 12, 4, 1, 4), 0, 0)
     TRK_ENTRY(tile(kR16, 1, 1, 10, 12, 2, 1, 4), 0, 0)
     // 4096 -> 14336, (16,16,16) -> (16,28,32), rank 8, bf16, chain (G1, G2, G3)
     TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 2, 2), 1, 1)
+    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 4, 1, 0, 16, 8), 0, 0)
+    TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 8, 1, 0, 16, 8), 0, 0)
     TRK_ENTRY(tile(kUp, 1, 1, 2, 32, 8, 4, 1), 0, 0)
     TRK_ENTRY(tile(kUp, 1, 1, 4, 32, 8, 2, 2), 0, 0)
     TRK_ENTRY(tile(kUp, 1, 1, 7, 32, 8, 1, 2), 0, 0)
@@ -32,6 +39,7 @@ const Entry kEntries[] = {
     TRK_ENTRY(tile(kUp, 1, 1, 28, 32, 8, 1, 2), 9, 64)
     // 14336 -> 4096, (16,28,32) -> (16,16,16), rank 16, bf16, chain (G3, G2, G1)
     TRK_ENTRY(tile(kDown, 1, 1, 1, 16, 2, 4, 1), 1, 1)
+    TRK_ENTRY(tile(kDown, 1, 1, 1, 16, 2, 8, 1, 0, 16, 8), 0, 0)
     TRK_ENTRY(tile(kDown, 1, 1, 2, 16, 2, 4, 1), 0, 0)
 };
 

@@ -195,3 +195,42 @@ def test_golden_vectors_fp32():
         expected = golden[f"{name}/y"]
         err = np.abs(y.double().cpu().numpy() - expected).max()
         assert err <= 1e-4 * max(1.0, np.abs(expected).max()), (name, err)
+
+
+# ---- the per-call path and graph capture ----------------------------------------------------
+def test_calls_take_the_native_path_and_fall_back_for_misaligned_x():
+    spec = TRSpec(rank=8)
+    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=6)
+    run = prepare_optimized(cores, spec)
+    x = gpu_x(spec, 3, 21, torch.float16)
+    y_native = run._call(run._bound, x)          # the C++ path of __call__ (allocate + launch)
+    assert y_native is not None and y_native.shape == (3, spec.out_features)
+    check_result(y_native, oracle_y(x, cores, spec), torch.float16)
+    flat = torch.empty(3 * spec.in_features + 1, device="cuda", dtype=torch.float16)
+    shifted = flat[1:].view(3, spec.in_features)  # 2-byte offset: not 16-byte aligned
+    shifted.copy_(x)
+    assert run._call(run._bound, shifted) is None  # left to the checked path, which copies
+    assert torch.equal(run(shifted), y_native)
+
+
+def test_graph_capture_replays_match_eager_calls():
+    spec = TRSpec(rank=8)
+    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=8)
+    run = prepare_optimized(cores, spec)
+    static_x = gpu_x(spec, 4, 30, torch.float16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run(static_x)                             # warm up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_y = run(static_x)
+    for replay in range(4):
+        announce(test="graph", replay=replay)
+        static_x.copy_(gpu_x(spec, 4, 31 + replay, torch.float16))
+        graph.replay()
+        eager = run(static_x.clone())             # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(static_y, eager), replay
+        check_result(static_y, oracle_y(static_x, cores, spec), torch.float16)
