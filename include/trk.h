@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRK_ABI_VERSION 1
+#define TRK_ABI_VERSION 2
 
 /* Element types of x, y and the cores. */
 enum trk_dtype { TRK_DTYPE_F16 = 0, TRK_DTYPE_BF16 = 1, TRK_DTYPE_F32 = 2 };
@@ -45,6 +45,22 @@ enum trk_status {
 
 /* Kernel families. */
 enum trk_kernel_kind { TRK_KERNEL_GENERIC = 0, TRK_KERNEL_MFMA = 1 };
+
+/* What a forward call writes for each output element, with v = (TR(cores) x)[t, o] as the
+ * kernel holds it (fp32 accumulator) and a = aux[t, o] (an optional [T][out] input in the
+ * plan's dtype or in fp32):
+ *   TRK_EPI_STORE     y[t,o] = v, in the plan's dtype (what trk_forward writes)
+ *   TRK_EPI_F32       y[t,o] = v, y in fp32 (no rounding to 16 bits)
+ *   TRK_EPI_ADD       y[t,o] = a + v, in the plan's dtype (residual add; aux may equal y)
+ *   TRK_EPI_SILU_MUL  y[t,o] = silu(a) * v = a / (1 + exp(-a)) * v, in the plan's dtype
+ *                     (the gate of a SwiGLU MLP; aux may equal y)
+ * The sums are formed in fp32 and rounded once. */
+enum trk_epilogue {
+    TRK_EPI_STORE = 0,
+    TRK_EPI_F32 = 1,
+    TRK_EPI_ADD = 2,
+    TRK_EPI_SILU_MUL = 3
+};
 
 typedef struct trk_plan trk_plan;
 
@@ -123,6 +139,30 @@ int trk_forward(const trk_plan *plan, const void *packed, const void *x, void *y
 /* trk_forward with an explicit variant index (parity tests of every variant, sweeps). */
 int trk_forward_variant(const trk_plan *plan, int variant, const void *packed, const void *x,
                         void *y, int tokens, void *stream);
+
+/* trk_forward with an epilogue (enum trk_epilogue) fused into the kernel's output store, with
+ * an explicit variant (-1 = the plan's selection for `tokens`). aux is [tokens][out] in
+ * aux_dtype (the plan's dtype or TRK_DTYPE_F32), 16-bit aligned, read only by
+ * TRK_EPI_ADD / TRK_EPI_SILU_MUL (NULL otherwise); y is fp32 for TRK_EPI_F32.
+ * Replaces forward_fp32 (csrc/v3g/bind.cu:84-92, PreparedTRKernel.accumulate,
+ * tr_kernel.py:230-243), which returns a view of the persistent fp32 workspace that the
+ * consumer must clear; here y is an ordinary output and nothing needs clearing. TRK_EPI_ADD
+ * and TRK_EPI_SILU_MUL fold consume_add / consume_silu_mul (bind.cu:96-149) into the
+ * producing kernel. */
+int trk_forward_epilogue(const trk_plan *plan, int variant, const void *packed, const void *x,
+                         void *y, int tokens, int epilogue, const void *aux, int aux_dtype,
+                         void *stream);
+
+/* out[i] = silu(g[i]) * u[i] for n elements: g and u fp32, out in out_dtype (rounded once).
+ * g and u are only read. Replaces consume_silu_mul (csrc/v3g/bind.cu:96-110, :126-136),
+ * which also zeroes g and u because they are its persistent workspace; nothing here is
+ * persistent, so nothing is cleared. */
+int trk_consume_silu_mul(const float *g, const float *u, void *out, int out_dtype, size_t n,
+                         void *stream);
+
+/* out[i] = h[i] + y[i] for n elements: h and out in `dtype`, y fp32 (rounded once); out may
+ * equal h. y is only read. Replaces consume_add (csrc/v3g/bind.cu:112-122, :138-149). */
+int trk_consume_add(const void *h, const float *y, void *out, int dtype, size_t n, void *stream);
 
 /* Launch floor: one empty kernel on `stream` (tr_ring.cu:1194-1200, empty_launch). */
 int trk_empty_launch(void *stream);

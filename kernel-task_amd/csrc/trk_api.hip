@@ -249,26 +249,63 @@ int trk_pack(const trk_plan *plan, const void *g1, const void *g2, const void *g
     return launch_pack(*as_plan(plan), g1, g2, g3, packed, static_cast<hipStream_t>(stream));
 }
 
-int trk_forward_variant(const trk_plan *plan, int variant, const void *packed, const void *x,
-                        void *y, int tokens, void *stream) {
+int trk_forward_epilogue(const trk_plan *plan, int variant, const void *packed, const void *x,
+                         void *y, int tokens, int epilogue, const void *aux, int aux_dtype,
+                         void *stream) {
     if (!plan) return set_error(TRK_ERR_INVALID, "trk_forward: null plan");
     const Plan &p = *as_plan(plan);
     if (tokens < 0) return set_error(TRK_ERR_INVALID, "trk_forward: tokens < 0");
-    if (tokens == 0) return TRK_OK;
-    if (!packed || !x || !y) return set_error(TRK_ERR_INVALID, "trk_forward: null buffer");
-    if (variant < 0 || variant >= p.nvariants)
+    if (epilogue < TRK_EPI_STORE || epilogue > TRK_EPI_SILU_MUL)
+        return set_error(TRK_ERR_INVALID, "trk_forward: unknown epilogue %d", epilogue);
+    const bool reads_aux = epilogue == TRK_EPI_ADD || epilogue == TRK_EPI_SILU_MUL;
+    if (reads_aux && aux_dtype != p.dtype && aux_dtype != TRK_DTYPE_F32)
+        return set_error(TRK_ERR_INVALID,
+                         "trk_forward: aux dtype %d is neither the plan's (%d) nor fp32",
+                         aux_dtype, p.dtype);
+    if (variant < 0) variant = trk_plan_select(plan, tokens);
+    if (variant >= p.nvariants)
         return set_error(TRK_ERR_INVALID, "trk_forward: no variant %d", variant);
+    if (tokens == 0) return TRK_OK;
+    if (!packed || !x || !y || (reads_aux && !aux))
+        return set_error(TRK_ERR_INVALID, "trk_forward: null buffer");
+    const int aux_align = reads_aux ? (aux_dtype == TRK_DTYPE_F32 ? 4 : p.elem) : 1;
+    const int y_align = epilogue == TRK_EPI_F32 ? 4 : p.elem;
+    if ((reinterpret_cast<uintptr_t>(aux) & (aux_align - 1)) ||
+        (reinterpret_cast<uintptr_t>(y) & (y_align - 1)))
+        return set_error(TRK_ERR_INVALID, "trk_forward: y or aux not aligned to its element");
     const Variant &v = p.variants[variant];
     if (v.kind == TRK_KERNEL_MFMA &&
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(packed)) & 15))
         return set_error(TRK_ERR_INVALID, "trk_forward: x and packed must be 16-byte aligned");
-    return v.launch(p, v, packed, x, y, tokens, static_cast<hipStream_t>(stream));
+    Epi epi{reads_aux ? aux : nullptr,
+            epilogue | (reads_aux && aux_dtype == TRK_DTYPE_F32 ? kAuxF32 : 0)};
+    return v.launch(p, v, packed, x, y, tokens, epi, static_cast<hipStream_t>(stream));
+}
+
+int trk_forward_variant(const trk_plan *plan, int variant, const void *packed, const void *x,
+                        void *y, int tokens, void *stream) {
+    if (variant < 0) return set_error(TRK_ERR_INVALID, "trk_forward: no variant %d", variant);
+    return trk_forward_epilogue(plan, variant, packed, x, y, tokens, TRK_EPI_STORE, nullptr,
+                                TRK_DTYPE_F16, stream);
 }
 
 int trk_forward(const trk_plan *plan, const void *packed, const void *x, void *y, int tokens,
                 void *stream) {
     if (!plan) return set_error(TRK_ERR_INVALID, "trk_forward: null plan");
     return trk_forward_variant(plan, trk_plan_select(plan, tokens), packed, x, y, tokens, stream);
+}
+
+int trk_consume_silu_mul(const float *g, const float *u, void *out, int out_dtype, size_t n,
+                         void *stream) {
+    if (n > 0 && (!g || !u || !out))
+        return set_error(TRK_ERR_INVALID, "trk_consume_silu_mul: null buffer");
+    return launch_silu_mul(g, u, out, out_dtype, n, static_cast<hipStream_t>(stream));
+}
+
+int trk_consume_add(const void *h, const float *y, void *out, int dtype, size_t n, void *stream) {
+    if (n > 0 && (!h || !y || !out))
+        return set_error(TRK_ERR_INVALID, "trk_consume_add: null buffer");
+    return launch_add(h, y, out, dtype, n, static_cast<hipStream_t>(stream));
 }
 
 int trk_empty_launch(void *stream) { return launch_empty(static_cast<hipStream_t>(stream)); }

@@ -35,7 +35,7 @@ template <int DT>
 __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
     const typename Elem<DT>::T *__restrict__ x, const typename Elem<DT>::T *__restrict__ Fk,
     const typename Elem<DT>::T *__restrict__ Sk, const typename Elem<DT>::T *__restrict__ Lk,
-    typename Elem<DT>::T *__restrict__ y, GenericArgs a) {
+    void *y, GenericArgs a, const void *aux, int epi_mode) {  // aux may equal y
     using E = Elem<DT>;
     extern __shared__ float lds[];
     const int R = a.R, RC = a.RC;
@@ -88,10 +88,11 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
                 }
             }
         }
-        typename E::T *yt = y + size_t(t) * a.out_features + size_t(f) * a.syF;
+        const size_t yt = size_t(t) * a.out_features + size_t(f) * a.syF;
         for (int idx = tid; idx < nY; idx += kThreads) {
             const int s = idx / a.oL, l = idx % a.oL;
-            yt[s * a.syS + l * a.syL] = E::from_f32(Y[idx]);
+            const size_t o = yt + s * a.syS + l * a.syL;
+            epi_put<DT>(y, epi_mode, o, Y[idx], epi_aux<DT>(aux, epi_mode, o));
         }
         __syncthreads();  // U of the next token is written after every thread left stage 2
     }
@@ -129,7 +130,7 @@ int generic_configure(const Plan &plan, int chain, Variant *v) {
 }
 
 int launch_generic(const Plan &plan, const Variant &v, const void *packed, const void *x,
-                   void *y, int tokens, hipStream_t stream) {
+                   void *y, int tokens, Epi epi, hipStream_t stream) {
     const Chain &c = plan.chains[v.chain];
     GenericArgs a;
     a.T = tokens;
@@ -160,7 +161,7 @@ int launch_generic(const Plan &plan, const Variant &v, const void *packed, const
         hipLaunchKernelGGL(ring3_generic_kernel<DT>, grid, dim3(kThreads), v.lds_bytes, stream, \
                            static_cast<const T *>(x), reinterpret_cast<const T *>(base + c.offF), \
                            reinterpret_cast<const T *>(base + c.offS),                         \
-                           reinterpret_cast<const T *>(base + c.offL), static_cast<T *>(y), a); \
+                           reinterpret_cast<const T *>(base + c.offL), y, a, epi.aux, epi.mode); \
         break;                                                                                 \
     }
         TRK_LAUNCH_GENERIC(TRK_DTYPE_F16)

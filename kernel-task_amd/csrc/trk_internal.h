@@ -36,8 +36,17 @@ struct Chain {
 struct Plan;
 struct Variant;
 
+// Output stage of a launch (enum trk_epilogue): `mode` is the epilogue kind, plus kAuxF32
+// when aux is fp32 rather than the plan's dtype.
+struct Epi {
+    const void *aux;
+    int mode;
+};
+constexpr int kEpiKindMask = 15;
+constexpr int kAuxF32 = 16;
+
 using LaunchFn = int (*)(const Plan &, const Variant &, const void *packed, const void *x,
-                         void *y, int tokens, hipStream_t stream);
+                         void *y, int tokens, Epi epi, hipStream_t stream);
 
 struct Variant {
     int kind;        // trk_kernel_kind
@@ -75,8 +84,12 @@ int launch_pack(const Plan &plan, const void *g1, const void *g2, const void *g3
                 hipStream_t stream);                                   // trk_pack.hip
 int generic_configure(const Plan &plan, int chain, Variant *v);       // trk_generic.hip
 int launch_generic(const Plan &plan, const Variant &v, const void *packed, const void *x,
-                   void *y, int tokens, hipStream_t stream);           // trk_generic.hip
+                   void *y, int tokens, Epi epi, hipStream_t stream);  // trk_generic.hip
 int launch_empty(hipStream_t stream);                                  // trk_generic.hip
+// elementwise consumers of fp32 outputs (trk_consume.hip)
+int launch_silu_mul(const float *g, const float *u, void *out, int out_dtype, size_t n,
+                    hipStream_t stream);
+int launch_add(const void *h, const float *y, void *out, int dtype, size_t n, hipStream_t stream);
 
 // MFMA variants compiled for this plan's shape: appends to plan->variants and returns how
 // many were added (trk_mfma_lds.hip: core slices in LDS; trk_mfma_wide.hip: in registers).

@@ -33,6 +33,7 @@
 #include <type_traits>
 
 #include "trk_internal.h"
+#include "trk_types.h"
 
 namespace trk {
 namespace {
@@ -489,13 +490,21 @@ __device__ __forceinline__ void reg_gemm32(const RegA32<O, BMW, K> &A, const typ
     }
 }
 
-template <KCfg C>
+// EPI: false compiles the plain store of the plan's dtype only (epi_mode is ignored); true
+// compiles every epilogue, chosen at run time by epi_mode. Two instantiations keep the plain
+// path's code exactly as it is without epilogues (measured: a run-time branch in its store
+// loop cost up to 0.8 us at tokens 8-32).
+template <KCfg C, bool EPI>
 __global__ void __launch_bounds__(Geo<C>::NT)
     ring3_mfma_kernel(const typename Ops<C.dt>::E *__restrict__ x,
                       const typename Ops<C.dt>::E *__restrict__ Fk,
                       const typename Ops<C.dt>::E *__restrict__ Sk,
-                      const typename Ops<C.dt>::E *__restrict__ Lk,
-                      typename Ops<C.dt>::E *__restrict__ y, int T) {
+                      const typename Ops<C.dt>::E *__restrict__ Lk, void *y, int T,
+                      int epi_mode, const void *aux) {  // aux may equal y
+    // The arguments fill 14 dwords, all of which arrive preloaded in SGPRs
+    // (-amdgpu-kernarg-preload-count): one more would be fetched from the kernel-argument
+    // segment, which lives in host memory when HIP_FORCE_DEV_KERNARG=0, and the first LDS
+    // wait (lgkmcnt also counts scalar loads) would stall on that PCIe read.
     using G = Geo<C>;
     using O = Ops<C.dt>;
     using E = typename O::E;
@@ -806,28 +815,56 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     }
     if (part3 != 0) return;
 
-    // write y[t, f, s, l] (permuted back to (p, q, r) by the compile-time strides)
-#pragma unroll
-    for (int j = 0; j < G::NYW; ++j) {
+    // write y[t, f, s, l] (permuted back to (p, q, r) by the compile-time strides) through
+    // the epilogue: the plan's dtype (its own unrolled loop of plain stores), or fp32, or
+    // fused with a residual add or a SiLU gate, whose inputs are all read before any store
+    auto y_at = [&](int j, int i, size_t *o) {
         const int tile = g3 + G::G3 * j;
-        if (tile >= G::NT3) continue;
         const int mt = tile / G::N3T, nt = tile % G::N3T;
-        const int l = nt * 16 + lrow;
-        if (l >= LCv) continue;
+        const int l = nt * 16 + lrow, m = mt * 16 + 4 * lgrp + i;
+        const int s = m % G::SC, f = (m / G::SC) % G::FC, t = m / (G::SC * G::FC);
+        *o = size_t(t0 + t) * G::OUT + (f0 + f) * G::SYF + (s0 + s) * G::SYS + (l0 + l) * G::SYL;
+        return tile < G::NT3 && l < LCv && m < G::M3 && s < SCv && f < FCv && t0 + t < T;
+    };
+    if constexpr (!EPI) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = mt * 16 + 4 * lgrp + i;
-            const int s = m % G::SC, f = (m / G::SC) % G::FC, t = m / (G::SC * G::FC);
-            if (m < G::M3 && s < SCv && f < FCv && t0 + t < T)
-                y[size_t(t0 + t) * G::OUT + (f0 + f) * G::SYF + (s0 + s) * G::SYS +
-                  (l0 + l) * G::SYL] = E(acc[j][0][i]);
+        for (int j = 0; j < G::NYW; ++j) {
+            const int tile = g3 + G::G3 * j;
+            if (tile >= G::NT3) continue;
+            const int mt = tile / G::N3T, nt = tile % G::N3T;
+            const int l = nt * 16 + lrow;
+            if (l >= LCv) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = mt * 16 + 4 * lgrp + i;
+                const int s = m % G::SC, f = (m / G::SC) % G::FC, t = m / (G::SC * G::FC);
+                if (m < G::M3 && s < SCv && f < FCv && t0 + t < T)
+                    static_cast<E *>(y)[size_t(t0 + t) * G::OUT + (f0 + f) * G::SYF +
+                                        (s0 + s) * G::SYS + (l0 + l) * G::SYL] = E(acc[j][0][i]);
+            }
         }
+    } else {
+        float a[G::NYW][4];
+#pragma unroll
+        for (int j = 0; j < G::NYW; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                size_t o;
+                a[j][i] = y_at(j, i, &o) ? epi_aux<C.dt>(aux, epi_mode, o) : 0.0f;
+            }
+#pragma unroll
+        for (int j = 0; j < G::NYW; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                size_t o;
+                if (y_at(j, i, &o)) epi_put<C.dt>(y, epi_mode, o, acc[j][0][i], a[j][i]);
+            }
     }
 }
 
 template <KCfg C>
 int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const void *x, void *y,
-                int tokens, hipStream_t stream) {
+                int tokens, Epi epi, hipStream_t stream) {
     using G = Geo<C>;
     using E = typename Ops<C.dt>::E;
     const Chain &c = plan.chains[v.chain];
@@ -836,10 +873,16 @@ int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const vo
     if (grid.y > 65535u)
         return set_error(TRK_ERR_UNSUPPORTED, "trk_forward: %d tokens exceed one launch of %s",
                          tokens, v.name);
-    hipLaunchKernelGGL(ring3_mfma_kernel<C>, grid, dim3(G::NT), 0, stream,
-                       static_cast<const E *>(x), reinterpret_cast<const E *>(base + c.offF),
-                       reinterpret_cast<const E *>(base + c.offS),
-                       reinterpret_cast<const E *>(base + c.offL), static_cast<E *>(y), tokens);
+    const E *xe = static_cast<const E *>(x);
+    const E *fk = reinterpret_cast<const E *>(base + c.offF);
+    const E *sk = reinterpret_cast<const E *>(base + c.offS);
+    const E *lk = reinterpret_cast<const E *>(base + c.offL);
+    if (epi.mode == TRK_EPI_STORE)
+        hipLaunchKernelGGL((ring3_mfma_kernel<C, false>), grid, dim3(G::NT), 0, stream, xe, fk, sk,
+                           lk, y, tokens, epi.mode, epi.aux);
+    else
+        hipLaunchKernelGGL((ring3_mfma_kernel<C, true>), grid, dim3(G::NT), 0, stream, xe, fk, sk,
+                           lk, y, tokens, epi.mode, epi.aux);
     return check_hip(hipGetLastError(), "trk_forward: MFMA kernel launch");
 }
 

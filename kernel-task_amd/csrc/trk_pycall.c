@@ -50,11 +50,37 @@ static PyObject *py_forward_variant(PyObject *self, PyObject *const *args, Py_ss
                                                (int)tokens, stream));
 }
 
+/* forward_epilogue(plan, variant, packed, x, y, tokens, epilogue, aux, aux_dtype, stream)
+ * -> status */
+static PyObject *py_forward_epilogue(PyObject *self, PyObject *const *args, Py_ssize_t n) {
+    void *plan, *packed, *x, *y, *aux, *stream;
+    (void)self;
+    if (n != 10) {
+        PyErr_SetString(PyExc_TypeError, "forward_epilogue(plan, variant, packed, x, y, tokens, "
+                                         "epilogue, aux, aux_dtype, stream)");
+        return NULL;
+    }
+    if (!as_ptr(args[0], &plan) || !as_ptr(args[2], &packed) || !as_ptr(args[3], &x) ||
+        !as_ptr(args[4], &y) || !as_ptr(args[7], &aux) || !as_ptr(args[9], &stream))
+        return NULL;
+    const long variant = PyLong_AsLong(args[1]);
+    const long tokens = PyLong_AsLong(args[5]);
+    const long epilogue = PyLong_AsLong(args[6]);
+    const long aux_dtype = PyLong_AsLong(args[8]);
+    if (PyErr_Occurred()) return NULL;
+    return PyLong_FromLong(trk_forward_epilogue((const trk_plan *)plan, (int)variant, packed, x,
+                                                y, (int)tokens, (int)epilogue, aux,
+                                                (int)aux_dtype, stream));
+}
+
 static PyMethodDef methods[] = {
     {"forward", (PyCFunction)(void (*)(void))py_forward, METH_FASTCALL,
      "trk_forward(plan, packed, x, y, tokens, stream) -> status"},
     {"forward_variant", (PyCFunction)(void (*)(void))py_forward_variant, METH_FASTCALL,
      "trk_forward_variant(plan, variant, packed, x, y, tokens, stream) -> status"},
+    {"forward_epilogue", (PyCFunction)(void (*)(void))py_forward_epilogue, METH_FASTCALL,
+     "trk_forward_epilogue(plan, variant, packed, x, y, tokens, epilogue, aux, aux_dtype, "
+     "stream) -> status"},
     {NULL, NULL, 0, NULL},
 };
 

@@ -30,6 +30,7 @@ struct Bound {
     const void *packed;
     int64_t in_features, out_features;
     c10::ScalarType dtype;
+    int dtype_code;  // the same dtype as an enum trk_dtype
     c10::DeviceIndex device;
 };
 
@@ -68,6 +69,7 @@ PyObject *py_bind(PyObject *, PyObject *const *args, Py_ssize_t n) {
         delete b;
         return nullptr;
     }
+    b->dtype_code = static_cast<int>(code);
     if (!b->plan || !b->packed || !scalar_type_of(code, &b->dtype)) {
         delete b;
         PyErr_SetString(PyExc_ValueError, "bind: null plan or packed buffer, or unknown dtype");
@@ -78,15 +80,24 @@ PyObject *py_bind(PyObject *, PyObject *const *args, Py_ssize_t n) {
     return capsule;
 }
 
-// forward(capsule, x) -> y, or None when x needs the checked path.
+// forward(capsule, x[, epilogue, aux]) -> y, or None when x or aux needs the checked path.
+// epilogue is an enum trk_epilogue (default TRK_EPI_STORE); y is fp32 for TRK_EPI_F32 and
+// in the plan's dtype otherwise; aux ([T, out], the plan's dtype or fp32, contiguous, on x's
+// device) is read by TRK_EPI_ADD and TRK_EPI_SILU_MUL.
 PyObject *py_forward(PyObject *, PyObject *const *args, Py_ssize_t n) {
     HANDLE_TH_ERRORS
-    if (n != 2) {
-        PyErr_SetString(PyExc_TypeError, "forward(bound, x)");
+    if (n != 2 && n != 4) {
+        PyErr_SetString(PyExc_TypeError, "forward(bound, x[, epilogue, aux])");
         return nullptr;
     }
     const auto *b = static_cast<const Bound *>(PyCapsule_GetPointer(args[0], kCapsule));
     if (!b) return nullptr;
+    int epilogue = TRK_EPI_STORE;
+    if (n == 4) {
+        epilogue = static_cast<int>(PyLong_AsLong(args[2]));
+        if (PyErr_Occurred()) return nullptr;
+        if (epilogue < TRK_EPI_STORE || epilogue > TRK_EPI_SILU_MUL) Py_RETURN_NONE;
+    }
     if (!THPVariable_Check(args[1])) Py_RETURN_NONE;
     const at::Tensor &x = THPVariable_Unpack(args[1]);
     if (x.scalar_type() != b->dtype || !x.is_cuda() || x.get_device() != b->device ||
@@ -94,11 +105,31 @@ PyObject *py_forward(PyObject *, PyObject *const *args, Py_ssize_t n) {
         !x.is_contiguous() || (reinterpret_cast<uintptr_t>(x.const_data_ptr()) & 15))
         Py_RETURN_NONE;
     const int64_t tokens = x.size(0);
-    at::Tensor y = at::empty({tokens, b->out_features}, x.options());
+    const void *aux_ptr = nullptr;
+    int aux_dtype = TRK_DTYPE_F32;
+    if (epilogue == TRK_EPI_ADD || epilogue == TRK_EPI_SILU_MUL) {
+        if (!THPVariable_Check(args[3])) Py_RETURN_NONE;
+        const at::Tensor &aux = THPVariable_Unpack(args[3]);
+        const bool f32 = aux.scalar_type() == c10::ScalarType::Float;
+        if ((!f32 && aux.scalar_type() != b->dtype) || !aux.is_cuda() ||
+            aux.get_device() != b->device || aux.dim() != 2 || aux.size(0) != tokens ||
+            aux.size(1) != b->out_features || !aux.is_contiguous())
+            Py_RETURN_NONE;
+        aux_ptr = aux.const_data_ptr();
+        if (!f32) aux_dtype = b->dtype_code;
+    }
+    at::Tensor y = at::empty({tokens, b->out_features},
+                             epilogue == TRK_EPI_F32 ? x.options().dtype(c10::ScalarType::Float)
+                                                     : x.options());
     if (tokens > 0) {
         const hipStream_t stream = c10::hip::getCurrentHIPStream(b->device).stream();
-        const int status = trk_forward(b->plan, b->packed, x.const_data_ptr(),
-                                       y.mutable_data_ptr(), static_cast<int>(tokens), stream);
+        const int status =
+            epilogue == TRK_EPI_STORE
+                ? trk_forward(b->plan, b->packed, x.const_data_ptr(), y.mutable_data_ptr(),
+                              static_cast<int>(tokens), stream)
+                : trk_forward_epilogue(b->plan, -1, b->packed, x.const_data_ptr(),
+                                       y.mutable_data_ptr(), static_cast<int>(tokens), epilogue,
+                                       aux_ptr, aux_dtype, stream);
         if (status != TRK_OK) {
             PyErr_SetString(PyExc_RuntimeError, trk_last_error());
             return nullptr;
@@ -112,7 +143,8 @@ PyMethodDef methods[] = {
     {"bind", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)()>(py_bind)),
      METH_FASTCALL, "bind(plan, packed, in_features, out_features, dtype, device) -> capsule"},
     {"forward", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)()>(py_forward)),
-     METH_FASTCALL, "forward(bound, x) -> y, or None when x needs the checked path"},
+     METH_FASTCALL,
+     "forward(bound, x[, epilogue, aux]) -> y, or None when x or aux needs the checked path"},
     {nullptr, nullptr, 0, nullptr},
 };
 

@@ -10,10 +10,11 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libtrk.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 KERNEL_GENERIC, KERNEL_MFMA = 0, 1
+EPI_STORE, EPI_F32, EPI_ADD, EPI_SILU_MUL = 0, 1, 2, 3
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM = 0, 1, 2, 3, 4
 
@@ -64,6 +65,11 @@ SIGNATURES = {
     "trk_forward": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p]),
     "trk_forward_variant": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int,
                                      _c_void_p]),
+    "trk_forward_epilogue": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int,
+                                      _c_int, _c_void_p, _c_int, _c_void_p]),
+    "trk_consume_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_size_t,
+                                      _c_void_p]),
+    "trk_consume_add": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_size_t, _c_void_p]),
     "trk_empty_launch": (_c_int, [_c_void_p]),
     "trk_empty_call": (_c_int, []),
 }

@@ -11,6 +11,11 @@ prepare time, a tiling/variant choice per token count) with its own mechanics:
            be used from several streams. Inputs that need checking or copying go through
            the Python path below, which raises or copies first.
 
+  epilogues accumulate(x) stores y in fp32; forward_add(x, h) and forward_silu_mul(x, g)
+           fuse a residual add or a SwiGLU gate into the kernel's output store
+           (trk_forward_epilogue). consume_silu_mul / consume_add are the standalone
+           elementwise forms of the reference's fp32-output consumers.
+
 Environment switch (read at prepare time, for sweeps): TRK_VARIANT=<index> routes every
 token count to that variant of the plan (indices from `PreparedTRKernel.variants()`).
 """
@@ -33,14 +38,15 @@ if _raw_stream is None:
 
 
 def _fast_forward():
-    """The CPython fast-call binding of trk_forward (built next to libtrk.so), else ctypes."""
+    """The CPython fast-call bindings of trk_forward, trk_forward_variant and
+    trk_forward_epilogue (built next to libtrk.so), else their ctypes bindings."""
     _lib.load()  # binds and version-checks libtrk.so first
     try:
         from . import _trkcall
     except ImportError:
         lib = _lib.load()
-        return lib.trk_forward, lib.trk_forward_variant
-    return _trkcall.forward, _trkcall.forward_variant
+        return lib.trk_forward, lib.trk_forward_variant, lib.trk_forward_epilogue
+    return _trkcall.forward, _trkcall.forward_variant, _trkcall.forward_epilogue
 
 
 def _torch_call():
@@ -93,7 +99,7 @@ class PreparedTRKernel:
                                             g[2].data_ptr(), self.packed.data_ptr(),
                                             current_stream_handle(self.device_index)))
             del g  # packing is stream-ordered before any later call on this stream
-        self._forward, self._forward_variant = _fast_forward()
+        self._forward, self._forward_variant, self._forward_epilogue = _fast_forward()
         self._plan_handle = self.plan.handle
         self._packed_ptr = self.packed.data_ptr()
         torch_call = _torch_call()
@@ -130,24 +136,128 @@ class PreparedTRKernel:
         y = self._call(self._bound, x)
         return y if y is not None else self._checked_call(x)
 
-    def _checked_call(self, x: torch.Tensor) -> torch.Tensor:
+    def accumulate(self, x: torch.Tensor) -> torch.Tensor:
+        """y = TR(cores) x in fp32, [T, out_features]: the kernel's accumulator stored without
+        rounding to 16 bits (reference: PreparedTRKernel.accumulate, tr_kernel.py:230-243,
+        which returns a view of its persistent workspace that the consumer must clear; this
+        returns an ordinary new tensor)."""
+        y = self._call(self._bound, x, _lib.EPI_F32, None)
+        return y if y is not None else self._checked_call(x, _lib.EPI_F32)
+
+    def forward_add(self, x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """residual + TR(cores) x in the cores' dtype, the add fused into the kernel's output
+        store and rounded once. residual: [T, out_features], the cores' dtype or fp32
+        (the reference's consume_add(h, accumulate(x)), csrc/v3g/bind.cu:112-122, as one
+        launch)."""
+        y = self._call(self._bound, x, _lib.EPI_ADD, residual)
+        return y if y is not None else self._checked_call(x, _lib.EPI_ADD, residual)
+
+    def forward_silu_mul(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        """silu(gate) * TR(cores) x in the cores' dtype, fused into the kernel's output
+        store: the up projection of a SwiGLU MLP consuming the gate projection's output
+        (fp32 from accumulate(), or the cores' dtype). The reference's
+        consume_silu_mul(g, u), csrc/v3g/bind.cu:96-110, folded into the u launch."""
+        y = self._call(self._bound, x, _lib.EPI_SILU_MUL, gate)
+        return y if y is not None else self._checked_call(x, _lib.EPI_SILU_MUL, gate)
+
+    def _check_aux(self, aux: torch.Tensor, tokens: int) -> tuple[torch.Tensor, int]:
+        if not isinstance(aux, torch.Tensor):
+            raise ValueError("the epilogue input must be a tensor")
+        if aux.dtype is not self.dtype and aux.dtype is not torch.float32:
+            raise ValueError(f"the epilogue input must be {self.dtype} or float32, got {aux.dtype}")
+        if aux.get_device() != self.device_index:
+            raise ValueError(f"the epilogue input must be on {self.device}, got {aux.device}")
+        if tuple(aux.shape) != (tokens, self.out_features):
+            raise ValueError(f"Expected the epilogue input with shape [{tokens}, "
+                             f"{self.out_features}], got {tuple(aux.shape)}")
+        return aux.contiguous(), _DTYPES[aux.dtype]
+
+    def _checked_call(self, x: torch.Tensor, epilogue: int = _lib.EPI_STORE,
+                      aux: torch.Tensor | None = None) -> torch.Tensor:
         x = self._check(x)
         tokens = x.shape[0]
-        y = x.new_empty((tokens, self.out_features))
+        aux_ptr, aux_dtype = 0, _DTYPES[self.dtype]
+        if epilogue in (_lib.EPI_ADD, _lib.EPI_SILU_MUL):
+            aux, aux_dtype = self._check_aux(aux, tokens)
+            aux_ptr = aux.data_ptr()
+        y_dtype = torch.float32 if epilogue == _lib.EPI_F32 else self.dtype
+        y = x.new_empty((tokens, self.out_features), dtype=y_dtype)
         if tokens:
-            status = self._forward(self._plan_handle, self._packed_ptr, x.data_ptr(),
-                                   y.data_ptr(), tokens, _raw_stream(self.device_index))
+            stream = _raw_stream(self.device_index)
+            if epilogue == _lib.EPI_STORE:
+                status = self._forward(self._plan_handle, self._packed_ptr, x.data_ptr(),
+                                       y.data_ptr(), tokens, stream)
+            else:
+                status = self._forward_epilogue(self._plan_handle, -1, self._packed_ptr,
+                                                x.data_ptr(), y.data_ptr(), tokens, epilogue,
+                                                aux_ptr, aux_dtype, stream)
             if status:
                 _lib.check(status)
         return y
 
-    def run_variant(self, x: torch.Tensor, variant: int) -> torch.Tensor:
-        """Forward through one explicit variant (tests and sweeps)."""
+    def run_variant(self, x: torch.Tensor, variant: int, epilogue: int = _lib.EPI_STORE,
+                    aux: torch.Tensor | None = None) -> torch.Tensor:
+        """Forward through one explicit variant, optionally with an epilogue (tests, sweeps)."""
         x = self._check(x)
         tokens = x.shape[0]
-        y = x.new_empty((tokens, self.out_features))
+        aux_ptr, aux_dtype = 0, _DTYPES[self.dtype]
+        if epilogue in (_lib.EPI_ADD, _lib.EPI_SILU_MUL):
+            aux, aux_dtype = self._check_aux(aux, tokens)
+            aux_ptr = aux.data_ptr()
+        y_dtype = torch.float32 if epilogue == _lib.EPI_F32 else self.dtype
+        y = x.new_empty((tokens, self.out_features), dtype=y_dtype)
         if tokens:
-            _lib.check(self._forward_variant(self._plan_handle, int(variant), self._packed_ptr,
-                                             x.data_ptr(), y.data_ptr(), tokens,
-                                             _raw_stream(self.device_index)))
+            _lib.check(self._forward_epilogue(self._plan_handle, int(variant), self._packed_ptr,
+                                              x.data_ptr(), y.data_ptr(), tokens, int(epilogue),
+                                              aux_ptr, aux_dtype, _raw_stream(self.device_index)))
         return y
+
+
+def _check_consumer_operand(name: str, t: torch.Tensor, dtype: torch.dtype | None,
+                            like: torch.Tensor) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a tensor on a ROCm (cuda) device")
+    if dtype is not None and t.dtype is not dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.shape != like.shape or t.device != like.device:
+        raise ValueError(f"{name} must match {tuple(like.shape)} on {like.device}, got "
+                         f"{tuple(t.shape)} on {t.device}")
+    return t.contiguous()
+
+
+def consume_silu_mul(g: torch.Tensor, u: torch.Tensor,
+                     out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """silu(g) * u for fp32 g and u of one shape, rounded once to out_dtype (default bf16).
+
+    Reference: consume_silu_mul (csrc/v3g/bind.cu:96-110, :126-136), which also zeroes g and
+    u because they are its persistent workspace; here g and u are only read. For the
+    operator's own outputs, PreparedTRKernel.forward_silu_mul fuses this into the kernel."""
+    g = _check_consumer_operand("g", g, torch.float32, g)
+    u = _check_consumer_operand("u", u, torch.float32, g)
+    if out_dtype not in _DTYPES:
+        raise ValueError(f"Unsupported output dtype {out_dtype}")
+    out = torch.empty(g.shape, dtype=out_dtype, device=g.device)
+    with torch.cuda.device(g.device):
+        _lib.check(_lib.load().trk_consume_silu_mul(
+            g.data_ptr(), u.data_ptr(), out.data_ptr(), _DTYPES[out_dtype], g.numel(),
+            current_stream_handle(g.device.index)))
+    return out
+
+
+def consume_add(h: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """h + y for h in fp16/bf16/fp32 and fp32 y of one shape, rounded once to h's dtype.
+
+    Reference: consume_add (csrc/v3g/bind.cu:112-122, :138-149), which also zeroes y (its
+    persistent workspace); here y is only read. PreparedTRKernel.forward_add fuses this
+    into the kernel for the operator's own outputs."""
+    if not isinstance(h, torch.Tensor) or h.dtype not in _DTYPES:
+        raise ValueError("h must be a float16, bfloat16 or float32 tensor")
+    h = _check_consumer_operand("h", h, None, h)
+    y = _check_consumer_operand("y", y, torch.float32, h)
+    out = torch.empty_like(h)
+    with torch.cuda.device(h.device):
+        _lib.check(_lib.load().trk_consume_add(
+            h.data_ptr(), y.data_ptr(), out.data_ptr(), _DTYPES[h.dtype], h.numel(),
+            current_stream_handle(h.device.index)))
+    return out
+

@@ -27,6 +27,10 @@ Functions and the reference lines they restate:
   chain_forward     the same operator contracted in any core order (F, S, L); the HIP
                     kernels use such orders, this is their CPU statement
   errors            max-abs / mean-abs / rel-L2 (benchmarks/benchmark.py:66-75)
+  silu              silu(a) = a * sigmoid(a), the gate of the reference's fp32-output
+                    consumer consume_silu_mul (src/factorized_inference/csrc/v3g/bind.cu:96-110)
+  epilogue          what an output store writes for an accumulated y: y itself, silu(a)*y
+                    (consume_silu_mul, bind.cu:96-110) or a + y (consume_add, bind.cu:112-122)
 
 Pinning (what makes each function trustworthy, see tests/test_oracle.py):
   tr_forward, dense_weight, dense_forward, forward_pieces, chain_forward: agree with the
@@ -36,6 +40,9 @@ Pinning (what makes each function trustworthy, see tests/test_oracle.py):
   trace_entry: the reference's own known-answer test (tests/test_correctness.py:80-91) and
   numpy.kron at rank 1. Also checked against the independent C restatement
   (oracle/ring_oracle.c) and the committed golden vectors (tests/golden/).
+  silu, epilogue: scipy.special.expit (an independent logistic function), the closed-form
+  identities silu(0) = 0, silu(a) - silu(-a) = a, silu(a) -> a and -> 0 at the far ends,
+  and planted mistakes (a flipped sign, a dropped factor) that must fail them.
 """
 from __future__ import annotations
 
@@ -43,8 +50,12 @@ import numpy as np
 
 __all__ = [
     "tr_forward", "dense_weight", "dense_forward", "trace_entry", "forward_pieces",
-    "kron_weight", "chain_forward", "errors", "flops_per_token", "CHAIN_ORDERS",
+    "kron_weight", "chain_forward", "errors", "flops_per_token", "CHAIN_ORDERS", "silu",
+    "epilogue", "EPILOGUES",
 ]
+
+# Output epilogues, named as the kernels' (include/trk.h: enum trk_epilogue).
+EPILOGUES = ("store", "f32", "add", "silu_mul")
 
 
 def _dims(cores):
@@ -210,3 +221,32 @@ def errors(actual, expected):
         "mean_absolute_error": float(d.mean()) if d.size else 0.0,
         "relative_l2_error": float(np.linalg.norm(d) / max(np.linalg.norm(e), 1e-12)),
     }
+
+
+def silu(a):
+    """silu(a) = a * sigmoid(a) = a / (1 + exp(-a)), float64, overflow-safe at both ends.
+
+    The gate of the SwiGLU MLP that the reference's consume_silu_mul applies to its fp32
+    gate output (src/factorized_inference/csrc/v3g/bind.cu:96-110: g / (1 + exp(-g)) * u)."""
+    a = np.asarray(a, dtype=np.float64)
+    e = np.exp(-np.abs(a))               # in (0, 1]: never overflows
+    sig = np.where(a >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+    return a * sig
+
+
+def epilogue(kind, y, aux=None):
+    """What an output store writes for accumulated values y (float64):
+      "store", "f32": y;  "add": aux + y (consume_add, bind.cu:112-122);
+      "silu_mul": silu(aux) * y (consume_silu_mul with u = y, bind.cu:96-110)."""
+    y = np.asarray(y, dtype=np.float64)
+    if kind in ("store", "f32"):
+        return y
+    aux = np.asarray(aux, dtype=np.float64)
+    if aux.shape != y.shape:
+        raise ValueError(f"aux {aux.shape} does not match y {y.shape}")
+    if kind == "add":
+        return aux + y
+    if kind == "silu_mul":
+        return silu(aux) * y
+    raise ValueError(f"unknown epilogue {kind!r}")
+

@@ -209,3 +209,57 @@ def test_error_metrics():
     assert e["max_absolute_error"] == 0.5
     assert e["mean_absolute_error"] == 0.25
     assert abs(e["relative_l2_error"] - 0.5 / np.sqrt(1.0 + 2.25)) < 1e-15
+
+
+# ---- epilogues: silu and the fused consumers -----------------------------------------------
+def test_silu_matches_an_independent_logistic_and_its_identities():
+    from scipy.special import expit
+
+    a = np.concatenate([np.linspace(-30.0, 30.0, 2001), [-800.0, -1e-30, 0.0, 1e-30, 800.0]])
+    s = orc.silu(a)
+    assert np.all(np.isfinite(s))
+    np.testing.assert_allclose(s, a * expit(a), rtol=1e-14, atol=1e-300)
+    assert orc.silu(0.0) == 0.0
+    np.testing.assert_allclose(s - orc.silu(-a), a, rtol=1e-13, atol=1e-13)  # silu(a)-silu(-a)=a
+    assert orc.silu(800.0) == 800.0 and abs(orc.silu(-800.0)) < 1e-300
+    assert abs(orc.silu(1.0) - 1.0 / (1.0 + np.exp(-1.0))) < 1e-16      # sigmoid(1) by hand
+
+
+def test_epilogues_compose_with_the_operator():
+    x, cores = make(SPECS[2], seed=5, tokens=4)
+    y = orc.tr_forward(x, cores)
+    rng = np.random.default_rng(6)
+    aux = rng.standard_normal(y.shape)
+    assert np.array_equal(orc.epilogue("store", y), y)
+    assert np.array_equal(orc.epilogue("f32", y), y)
+    assert np.array_equal(orc.epilogue("add", y, aux), aux + y)
+    # a SwiGLU block: silu(gate) * up, elementwise, equals silu(gate) scaled per element
+    from scipy.special import expit
+    np.testing.assert_allclose(orc.epilogue("silu_mul", y, aux), aux * expit(aux) * y,
+                               rtol=1e-13, atol=1e-13)
+    # linearity of the operator carries through: silu_mul(g, y1 + y2) = silu_mul(g,y1)+(g,y2)
+    x2 = rng.standard_normal(x.shape)
+    y2 = orc.tr_forward(x2, cores)
+    lhs = orc.epilogue("silu_mul", orc.tr_forward(x + x2, cores), aux)
+    np.testing.assert_allclose(lhs, orc.epilogue("silu_mul", y, aux) + orc.epilogue("silu_mul", y2, aux),
+                               rtol=1e-11, atol=1e-11)
+    with pytest.raises(ValueError):
+        orc.epilogue("add", y, aux[:1])
+    with pytest.raises(ValueError):
+        orc.epilogue("relu", y, aux)
+
+
+@pytest.mark.parametrize("mistake", [
+    lambda a: a / (1.0 + np.exp(a)),            # flipped sign in the exponent
+    lambda a: 1.0 / (1.0 + np.exp(-a)),         # sigmoid without the factor a
+    lambda a: a * (1.0 / (1.0 + np.exp(-2 * a))),  # wrong slope
+])
+def test_planted_silu_mistakes_fail_the_identities(mistake):
+    a = np.linspace(-6.0, 6.0, 121)
+    with np.errstate(over="ignore"):
+        s = mistake(a)
+    ok_pair = np.allclose(s - mistake(-a), a, rtol=1e-12, atol=1e-12)
+    from scipy.special import expit
+    ok_ref = np.allclose(s, a * expit(a), rtol=1e-12, atol=1e-12)
+    assert not (ok_pair and ok_ref)
+
