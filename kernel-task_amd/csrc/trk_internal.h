@@ -95,5 +95,8 @@ int launch_add(const void *h, const float *y, void *out, int dtype, size_t n, hi
 // many were added (trk_mfma_lds.hip: core slices in LDS; trk_mfma_wide.hip: in registers).
 int mfma_register_lds(Plan *plan);
 int mfma_register_wide(Plan *plan);
+// Generated tables for the declared shapes (csrc/gen/, written by
+// factorized_inference/tilegen.py): appends the matching shape's variants.
+int mfma_register_generated(Plan *plan);
 
 }  // namespace trk

@@ -42,7 +42,19 @@ FILE_FLAGS: dict[str, list[str]] = {}
 
 
 def sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip"))
+    """Every HIP source: the hand-written ones and the generated variant tables (csrc/gen/,
+    rewritten from tilegen.py's declared shapes and tuned table first)."""
+    from . import tilegen
+
+    tilegen.write_all()
+    return sorted(CSRC.glob("*.hip")) + sorted((CSRC / "gen").glob("*.hip"))
+
+
+def _newest_dependency() -> float:
+    """Modification time of the newest header and of this build script (a change to either
+    recompiles every source)."""
+    deps = [*CSRC.glob("*.h"), *INCLUDE.glob("*.h"), Path(__file__)]
+    return max(p.stat().st_mtime for p in deps)
 
 
 def _hipcc() -> str:
@@ -51,12 +63,17 @@ def _hipcc() -> str:
     return str(path) if path.exists() else "hipcc"
 
 
-def build(verbose: bool = False, jobs: int = 8) -> Path:
+def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Path:
+    """Compile every source and link libtrk.so and the two bindings. incremental=True
+    (development only) reuses objects newer than their source, the headers and this script."""
     OBJ_DIR.mkdir(exist_ok=True)
     hipcc = _hipcc()
 
     def compile_one(src: Path) -> Path:
         obj = OBJ_DIR / (src.stem + ".o")
+        if (incremental and obj.exists()
+                and obj.stat().st_mtime > max(_newest_dependency(), src.stat().st_mtime)):
+            return obj
         cmd = [hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -108,4 +125,4 @@ def _build_torchcall(verbose: bool) -> None:
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv[1:]))
+    print(build(verbose="-v" in sys.argv[1:], incremental="--incremental" in sys.argv[1:]))

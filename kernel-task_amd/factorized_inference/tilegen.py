@@ -1,0 +1,411 @@
+"""Tile generator: MFMA variant tables for declared operator shapes.
+
+    python -m factorized_inference.tilegen            (from kernel-task_amd/; writes csrc/gen/)
+
+The MFMA kernel (csrc/trk_mfma_kernel.h) is compiled per shape and workgroup tile. The
+four BASELINE shapes have hand-tuned tables (csrc/trk_mfma_lds.hip, trk_mfma_wide.hip); every
+shape declared in DECLARED below gets a generated table instead:
+
+  1. chain order: the order (F, S, L) with the least MFMA work after padding (stage-1 K to
+     16, the second core's input mode to 16 rows, stage-2 K to 16, the last core's outputs to
+     16), ties to the order with the least unpadded work;
+  2. candidate tiles: single-token tiles that split the ring over many workgroups, mid-size
+     tiles that own all second-core outputs, and register-resident (WIDE) tiles with
+     32x32x16 stage-2 MFMAs for large token counts; each checked against the kernel's
+     compile-time constraints, its 160 KB LDS budget and a register estimate;
+  3. token ranges: from the autotuner's measurements (csrc/gen/tuned.json, written by
+     kernel-task_amd/benchmarks/autotune.py on an MI355X) when they exist, else a rule.
+     Once a shape is tuned, only the tiles that won a token range are compiled.
+
+Role of the reference's V3G generators (tools/gen_v3g_tilings.py, tools/gen_v3g_tuned.py,
+src/factorized_inference/v3g_tuned.py:4-17): a compiled variant list for the Qwen3.8-27B
+layer shapes (tools/qwen_shapes.py:20-27) and a measured table of the fastest tiling per
+token count. Own design: the tile space, the checks and the table format are this
+kernel's.
+"""
+from __future__ import annotations
+
+import json
+from dataclasses import asdict, dataclass, field
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+CSRC = PACKAGE.parent / "csrc"
+GEN_DIR = CSRC / "gen"
+TUNED = GEN_DIR / "tuned.json"
+
+DTYPES = {"f16": "TRK_DTYPE_F16", "bf16": "TRK_DTYPE_BF16"}
+LDS_LIMIT = 160 * 1024
+# registers a wave may give to the register-resident core slices (4 waves: one wave per
+# SIMD; 8 waves: two per SIMD, half the register file each)
+WIDE_VGPR_BUDGET = {4: 136, 8: 128}
+ORDERS = ((0, 1, 2), (1, 2, 0), (2, 0, 1), (0, 2, 1), (1, 0, 2), (2, 1, 0))
+
+
+def cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def rup(a: int, b: int) -> int:
+    return cdiv(a, b) * b
+
+
+@dataclass(frozen=True)
+class ShapeDecl:
+    """One operator shape to compile MFMA variants for."""
+
+    name: str
+    ins: tuple
+    outs: tuple
+    rank: int
+    dtype: str = "bf16"
+
+    @property
+    def key(self) -> str:
+        i, o = self.ins, self.outs
+        return (f"{self.dtype}_{i[0]}x{i[1]}x{i[2]}_{o[0]}x{o[1]}x{o[2]}_r{self.rank}")
+
+
+@dataclass(frozen=True)
+class Tile:
+    """Workgroup tile of ring3_mfma (csrc/trk_mfma_kernel.h, struct KCfg)."""
+
+    TT: int
+    FC: int
+    SC: int
+    LC: int
+    IC: int
+    KS3: int
+    NACC: int
+    WIDE: int = 0
+    MF2: int = 16
+    NW: int = 4
+
+    def args(self) -> str:
+        """Arguments of tile(shape, ...) in the variant tables."""
+        a = [self.TT, self.FC, self.SC, self.LC, self.IC, self.KS3, self.NACC]
+        if (self.WIDE, self.MF2, self.NW) != (0, 16, 4):
+            a += [self.WIDE, self.MF2, self.NW]
+        return ", ".join(map(str, a))
+
+
+# The linear layers of Qwen3.8-27B as tensor-ring shapes, the reference's own list
+# (tools/qwen_shapes.py:20-27), at ring ranks 8 and 16 in bf16 (tools/qwen_bench.py).
+QWEN = {
+    "mlp_gate_up": ((20, 16, 16), (16, 34, 32)),
+    "mlp_down": ((34, 32, 16), (16, 16, 20)),
+    "attn_q_gate": ((20, 16, 16), (16, 24, 32)),
+    "attn_kv": ((20, 16, 16), (8, 8, 16)),
+    "o_proj": ((24, 16, 16), (16, 16, 20)),
+    "gdn_qkvz": ((20, 16, 16), (16, 32, 32)),
+}
+DECLARED = [ShapeDecl(f"qwen_{name}", ins, outs, rank)
+            for name, (ins, outs) in QWEN.items() for rank in (8, 16)]
+
+
+@dataclass
+class Chain:
+    order: tuple
+    nF: int
+    nS: int
+    nL: int
+    oF: int
+    oS: int
+    oL: int
+    IN: int
+    xrow: bool = field(default=False)
+
+
+def chain_of(shape: ShapeDecl, order: tuple) -> Chain:
+    F, S, L = order
+    n, o = shape.ins, shape.outs
+    return Chain(order, n[F], n[S], n[L], o[F], o[S], o[L], n[0] * n[1] * n[2], xrow=F == 2)
+
+
+def padded_work(shape: ShapeDecl, order: tuple) -> tuple[int, int]:
+    """(MFMA multiply-adds per token after padding, unpadded multiply-adds per token) of
+    the three stages when one workgroup owns all second- and last-core outputs."""
+    c, R = chain_of(shape, order), shape.rank
+    s1 = c.oF * R * R * c.nL * rup(c.nS, 16) * rup(c.nF, 16)
+    s2 = c.oS * R * c.nL * R * c.oF * rup(c.nS * R, 16)
+    s3 = c.oF * c.oS * rup(c.oL, 16) * c.nL * R * R
+    u1 = c.IN * c.oF * R * R
+    u2 = c.nS * c.nL * c.oF * c.oS * R ** 3
+    u3 = c.nL * c.oF * c.oS * c.oL * R * R
+    return s1 + s2 + s3, u1 + u2 + u3
+
+
+def choose_order(shape: ShapeDecl) -> tuple:
+    return min(ORDERS, key=lambda o: padded_work(shape, o))
+
+
+def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
+    """The kernel's compile-time geometry (struct Geo) for one tile, with the reason the
+    kernel would reject it ("" when it compiles). Mirrors the static_asserts of Geo."""
+    c, R = chain_of(shape, order), shape.rank
+    R2 = R * R
+    g = {}
+    KF, K2, nSP = rup(c.nF, 16), rup(c.nS * R, 16), rup(c.nS, 16)
+    M1 = t.FC * R2
+    M1T = M1 // 16
+    N1 = t.IC * t.TT * nSP
+    M2 = t.SC * R
+    M2T = cdiv(M2, 16)
+    M2P = M2T * 16
+    N2 = t.IC * R * t.TT * t.FC
+    N2T = cdiv(N2, 16)
+    N2P = N2T * 16
+    M3 = t.TT * t.FC * t.SC
+    M3T = cdiv(M3, 16)
+    M3P = M3T * 16
+    N3T = cdiv(t.LC, 16)
+    LCP = N3T * 16
+    K3 = t.IC * R2
+    NW = t.NW
+    NT3 = M3T * N3T
+    wide = t.WIDE != 0
+    W32 = wide and t.MF2 == 32
+    WM2 = t.WIDE if wide else NW
+    G3 = NW // t.KS3 if t.KS3 and NW % t.KS3 == 0 else 1
+    NYW = cdiv(NT3, G3)
+    PF, P2, P3, PL = KF + 8, K2 + 8, K3 + 8, R2 + 8
+    M2T32, N2T32 = cdiv(M2, 32), cdiv(N2, 32)
+    BM1 = cdiv(M1T, NW)
+    BM2 = cdiv(M2T32 if W32 else M2T, WM2)
+    N2R = N2T32 * 32 if W32 else N2P
+    sz = {
+        "Fs": 8 if wide else M1 * PF,
+        "Ss": 8 if wide else M2P * P2,
+        "Ls": t.IC * LCP * PL,
+        "Xs": N1 * PF,
+        "Ub": N2R * P2,
+        "Vb": M3P * P3,
+    }
+    lds = 2 * sum(sz.values())
+    red_floats = (t.KS3 - 1) * G3 * NYW * 256
+    k3steps = K3 // 32 if K3 % 32 == 0 else 0
+    perk = k3steps // t.KS3 if t.KS3 else 0
+    qb = min(perk, 16)
+    g.update(LDS_BYTES=lds, NBLK=cdiv(c.oF, t.FC) * cdiv(c.oS, t.SC) * cdiv(c.oL, t.LC),
+             NSTEP=cdiv(c.nL, t.IC), BM1=BM1, BM2=BM2, NYW=NYW, K2=K2, KF=KF)
+    # register-resident slices (WIDE): A fragments held by each wave
+    if wide:
+        fa = BM1 * (KF // 32 * 4 + (2 if KF % 32 else 0))
+        sa = BM2 * (K2 // 16) * 4 if W32 else BM2 * (K2 // 32 * 4 + (2 if K2 % 32 else 0))
+        g["slice_vgprs"] = fa + sa
+    checks = [
+        (R % 8 == 0 and R & (R - 1) == 0, "rank must be a power of two >= 8"),
+        (NW in (4, 8), "4 or 8 waves"),
+        (0 <= t.WIDE <= NW and (t.WIDE == 0 or NW % t.WIDE == 0), "WIDE divides the waves"),
+        (t.MF2 == 16 or (t.MF2 == 32 and wide), "MF2 is 16, or 32 with WIDE"),
+        (16 % (t.FC * t.TT) == 0, "FC * TT must divide 16"),
+        (t.KS3 >= 1 and NW % t.KS3 == 0, "KS3 must divide the waves"),
+        (k3steps > 0 and k3steps % t.KS3 == 0, "stage-3 K steps must split over KS3"),
+        (t.NACC >= 1 and perk % t.NACC == 0, "NACC must divide a wave's K steps"),
+        (qb > 0 and perk % qb == 0 and qb % t.NACC == 0, "stage-3 batches must divide"),
+        (t.FC <= c.oF and t.SC <= c.oS and t.LC <= c.oL and t.IC <= c.nL and t.TT >= 1,
+         "tile too large"),
+        (c.nL % t.IC == 0, "IC must divide the last core's input mode"),
+        (c.xrow or c.IN % 8 == 0, "scatter loader reads x rows in 8-element vectors"),
+        (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
+        (red_floats * 4 <= sz["Ub"] * 2, "stage-3 reduction does not fit in Ub"),
+        (not wide or g["slice_vgprs"] <= WIDE_VGPR_BUDGET[NW], "register-resident slices too large"),
+    ]
+    g["reject"] = next((why for ok, why in checks if not ok), "")
+    return g
+
+
+def _divisors_desc(n: int) -> list[int]:
+    return [d for d in range(n, 0, -1) if n % d == 0]
+
+
+def _fit(shape, order, make, ics) -> Tile | None:
+    """The first tile make(ic) over ics that the kernel accepts."""
+    for ic in ics:
+        t = make(ic)
+        if t is not None and not geometry(shape, order, t)["reject"]:
+            return t
+    return None
+
+
+def candidates(shape: ShapeDecl, order: tuple | None = None) -> dict[str, Tile]:
+    """Named candidate tiles for one shape (each accepted by the kernel's constraints)."""
+    order = order or choose_order(shape)
+    c, R = chain_of(shape, order), shape.rank
+    ics = _divisors_desc(c.nL)
+    # K3 = IC * R^2 of 512-1024 keeps the per-step LDS traffic balanced at one token
+    small_ics = [d for d in ics if d * R * R <= 1024] or ics[-1:]
+    out: dict[str, Tile] = {}
+
+    def add(name, make, pool):
+        t = _fit(shape, order, make, pool)
+        if t is not None and t not in out.values():
+            out[name] = t
+
+    LC = c.oL
+    # one token: the ring split over many workgroups, stage 3's K split over the waves
+    add("t1_s1", lambda ic: Tile(1, 1, 1, LC, ic, 4, 1), small_ics)
+    add("t1_s2", lambda ic: Tile(1, 1, min(2, c.oS), LC, ic, 4, 1), small_ics)
+    add("t1_s1_w8", lambda ic: Tile(1, 1, 1, LC, ic, 8, 1, 0, 16, 8), small_ics)
+    # a few tokens: a workgroup owns half or all of the second core's outputs
+    half = cdiv(c.oS, 2)
+    add("mid_half", lambda ic: Tile(1, 1, half, LC, ic, 1, 2), ics)
+    add("mid_all", lambda ic: Tile(1, 1, c.oS, LC, ic, 1, 2), ics)
+    # many tokens: register-resident core slices, 4 tokens per workgroup, 32x32 stage 2
+    for wide, nw in ((4, 4), (8, 8)):
+        budget = WIDE_VGPR_BUDGET[nw]
+        best = None
+        for sc_max in range(c.oS, 0, -1):
+            chunks = cdiv(c.oS, sc_max)
+            sc = cdiv(c.oS, chunks)  # balanced chunks
+            t = _fit(shape, order, lambda ic, sc=sc: Tile(4, 1, sc, LC, ic, 2, 1, wide, 32, nw),
+                     [d for d in ics if d <= 2] or ics[-1:])
+            if t is not None and geometry(shape, order, t).get("slice_vgprs", 0) <= budget:
+                best = t
+                break
+        if best is not None and best not in out.values():
+            out[f"wide{wide}x32" + ("w8" if nw == 8 else "")] = best
+    return out
+
+
+def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
+    """Default token ranges before the shape is tuned."""
+    ranges = {}
+    pick = lambda *opts: next((o for o in opts if o in names), None)  # noqa: E731
+    t1 = ("t1_s2", "t1_s1", "t1_s1_w8")
+    for name, lo, hi in ((pick(*t1, "mid_half", "mid_all", "wide4x32", "wide8x32w8"), 1, 1),
+                         (pick("mid_half", "mid_all", "wide4x32", "wide8x32w8", *t1), 2, 16),
+                         (pick("mid_all", "mid_half", "wide4x32", "wide8x32w8", *t1), 17, 64),
+                         (pick("wide8x32w8", "wide4x32", "mid_all", "mid_half", *t1), 65,
+                          1 << 30)):
+        if name is None:
+            continue
+        if name in ranges:  # extend the range a tile already serves
+            ranges[name] = (min(ranges[name][0], lo), max(ranges[name][1], hi))
+        else:
+            ranges[name] = (lo, hi)
+    return ranges
+
+
+def load_tuned() -> dict:
+    return json.loads(TUNED.read_text()) if TUNED.exists() else {}
+
+
+def table(shape: ShapeDecl, tuned: dict | None = None) -> tuple[tuple, list[tuple[str, Tile, int, int]]]:
+    """(order, [(name, tile, t_min, t_max)]) for one shape: the tuned winners when the shape
+    has measurements, else every candidate with the rule's ranges (0, 0: index only)."""
+    tuned = load_tuned() if tuned is None else tuned
+    entry = tuned.get(shape.key)
+    if entry:
+        order = tuple(entry["order"])
+        rows = [(r["name"], Tile(**r["tile"]), r["t_min"], r["t_max"]) for r in entry["ranges"]]
+        for name, t, _, _ in rows:
+            why = geometry(shape, order, t)["reject"]
+            if why:
+                raise ValueError(f"{shape.key}: tuned tile {name} is rejected: {why}")
+        return order, rows
+    order = choose_order(shape)
+    cands = candidates(shape, order)
+    ranges = rule_ranges(list(cands))
+    return order, [(n, t, *ranges.get(n, (0, 0))) for n, t in cands.items()]
+
+
+def _fn_name(shape: ShapeDecl) -> str:
+    return "mfma_register_gen_" + shape.key
+
+
+def emit(shape: ShapeDecl, tuned: dict | None = None) -> str:
+    order, rows = table(shape, tuned)
+    i, o = shape.ins, shape.outs
+    tuned_note = ("token ranges measured by kernel-task_amd/benchmarks/autotune.py"
+                  if (load_tuned() if tuned is None else tuned).get(shape.key)
+                  else "token ranges by rule (not yet tuned)")
+    lines = [
+        "// Generated by kernel-task_amd/factorized_inference/tilegen.py; do not edit.",
+        f"// {shape.name}: ({i[0]},{i[1]},{i[2]}) -> ({o[0]},{o[1]},{o[2]}), rank "
+        f"{shape.rank}, {shape.dtype}, chain order ({order[0]},{order[1]},{order[2]}); "
+        f"{tuned_note}.",
+        '#include "trk_mfma_kernel.h"',
+        "",
+        "namespace trk {",
+        "namespace {",
+        "",
+        f"constexpr Shape kShape{{{DTYPES[shape.dtype]}, {order[0]}, {order[1]}, {order[2]}, "
+        f"{i[0]}, {i[1]}, {i[2]}, {o[0]}, {o[1]}, {o[2]}, {shape.rank}}};",
+        "",
+        "const Entry kEntries[] = {",
+    ]
+    for name, t, lo, hi in rows:
+        lines.append(f"    TRK_ENTRY(tile(kShape, {t.args()}), {lo}, {hi})  // {name}")
+    lines += [
+        "};",
+        "",
+        "}  // namespace",
+        "",
+        f"int {_fn_name(shape)}(Plan *plan) {{",
+        "    return register_entries(plan, kEntries, int(sizeof(kEntries) / sizeof(kEntries[0])));",
+        "}",
+        "",
+        "}  // namespace trk",
+        "",
+    ]
+    return "\n".join(lines)
+
+
+def emit_index(shapes: list[ShapeDecl]) -> str:
+    lines = [
+        "// Generated by kernel-task_amd/factorized_inference/tilegen.py; do not edit.",
+        "// Registers the generated MFMA variant tables (one translation unit per shape).",
+        '#include "trk_internal.h"',
+        "",
+        "namespace trk {",
+        "",
+    ]
+    lines += [f"int {_fn_name(s)}(Plan *plan);" for s in shapes]
+    lines += ["", "int mfma_register_generated(Plan *plan) {", "    int added = 0;"]
+    lines += [f"    added += {_fn_name(s)}(plan);" for s in shapes]
+    lines += ["    return added;", "}", "", "}  // namespace trk", ""]
+    return "\n".join(lines)
+
+
+def write_all(shapes: list[ShapeDecl] = DECLARED, out_dir: Path = GEN_DIR) -> list[Path]:
+    """Write one translation unit per shape plus the index; stale generated units are
+    removed. Returns the written sources."""
+    out_dir.mkdir(parents=True, exist_ok=True)
+    tuned = load_tuned()
+    written = []
+    for s in shapes:
+        p = out_dir / f"trk_gen_{s.key}.hip"
+        text = emit(s, tuned)
+        if not p.exists() or p.read_text() != text:
+            p.write_text(text)
+        written.append(p)
+    index = out_dir / "trk_gen_index.hip"
+    text = emit_index(shapes)
+    if not index.exists() or index.read_text() != text:
+        index.write_text(text)
+    written.append(index)
+    keep = {p.name for p in written}
+    for stale in out_dir.glob("trk_gen_*.hip"):
+        if stale.name not in keep:
+            stale.unlink()
+    return written
+
+
+def describe(shapes: list[ShapeDecl] = DECLARED) -> list[dict]:
+    """Per shape: order, work and the tiles with their geometry (for reports and tests)."""
+    out = []
+    for s in shapes:
+        order, rows = table(s)
+        padded, unpadded = padded_work(s, order)
+        out.append({"shape": s.key, "name": s.name, "order": order,
+                    "padded_mac_per_token": padded, "mac_per_token": unpadded,
+                    "tiles": [{"name": n, "tile": asdict(t), "t_min": lo, "t_max": hi,
+                               **{k: v for k, v in geometry(s, order, t).items()}}
+                              for n, t, lo, hi in rows]})
+    return out
+
+
+if __name__ == "__main__":
+    for path in write_all():
+        print(path)

@@ -1,0 +1,109 @@
+"""CPU checks of the tile generator (factorized_inference/tilegen.py).
+
+- The generator's mirror of the kernel's compile-time geometry agrees with the compiled
+  library: for every MFMA variant of every plan (hand-written and generated tables) the LDS
+  bytes match and the kernel's constraints accept the tile.
+- The committed generated sources are what the generator writes now.
+- Every declared shape gets MFMA variants whose default token ranges cover every token
+  count, in the chain order the generator chose.
+- Planted mistakes in a tile (a rank that is not a power of two, FC*TT not dividing 16, IC
+  not dividing the last core's input mode, LDS over budget) are rejected.
+"""
+from __future__ import annotations
+
+import re
+
+import numpy as np
+import pytest
+
+from factorized_inference import _lib, tilegen
+
+NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?|(_w8))?<(\d)(\d)(\d),"
+                  r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
+HAND = [
+    tilegen.ShapeDecl("r8", (8, 12, 20), (12, 10, 24), 8, "f16"),
+    tilegen.ShapeDecl("r16", (8, 12, 20), (12, 10, 24), 16, "f16"),
+    tilegen.ShapeDecl("up", (16, 16, 16), (16, 28, 32), 8, "bf16"),
+    tilegen.ShapeDecl("down", (16, 28, 32), (16, 16, 16), 16, "bf16"),
+]
+DT = {"f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16}
+
+
+def parse(name: str):
+    m = NAME.fullmatch(name)
+    assert m, name
+    wide = int(m.group(1) or 0)
+    order = tuple(int(m.group(i)) for i in (5, 6, 7))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(8, 15))
+    tile = tilegen.Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
+                        8 if (m.group(3) or m.group(4)) else 4)
+    return order, tile
+
+
+@pytest.mark.parametrize("shape", HAND + tilegen.DECLARED, ids=lambda s: s.key)
+def test_geometry_mirror_matches_the_library(shape):
+    plan = _lib.Plan(shape.ins, shape.outs, shape.rank, DT[shape.dtype])
+    mfma = [v for v in plan.variants(1) if v["kind"] == "mfma"]
+    assert mfma
+    for v in mfma:
+        order, tile = parse(v["name"])
+        g = tilegen.geometry(shape, order, tile)
+        assert g["LDS_BYTES"] == v["lds_bytes"], v["name"]
+        # the hand tables hold a few register-heavy sweep variants beyond the generator's
+        # register budget; every other constraint holds for all compiled tiles
+        assert g["reject"] in ("", "register-resident slices too large"), (v["name"], g["reject"])
+        assert list(order) == v["order"]
+
+
+def test_generated_sources_are_current(tmp_path):
+    written = tilegen.write_all(out_dir=tmp_path)
+    for p in written:
+        committed = tilegen.GEN_DIR / p.name
+        assert committed.exists(), f"{p.name} is not generated in csrc/gen"
+        assert committed.read_text() == p.read_text(), f"{p.name} is stale: rerun tilegen"
+
+
+@pytest.mark.parametrize("shape", tilegen.DECLARED, ids=lambda s: s.key)
+def test_declared_shapes_are_covered(shape):
+    order, rows = tilegen.table(shape)
+    plan = _lib.Plan(shape.ins, shape.outs, shape.rank, DT[shape.dtype])
+    for T in (1, 2, 3, 7, 8, 16, 17, 33, 64, 65, 128, 256, 4096):
+        info = plan.describe(-1, T)
+        assert info["kind"] == "mfma", (shape.key, T)
+        assert tuple(info["order"]) == order
+    for _, tile, lo, hi in rows:
+        assert not tilegen.geometry(shape, order, tile)["reject"]
+        assert (lo, hi) == (0, 0) or 1 <= lo <= hi
+
+
+def test_order_choice_prefers_least_padded_work():
+    for shape in tilegen.DECLARED + HAND:
+        best = tilegen.choose_order(shape)
+        work = {o: tilegen.padded_work(shape, o) for o in tilegen.ORDERS}
+        assert work[best] == min(work.values())
+    # the chosen order never does more unpadded work than twice the least
+    for shape in tilegen.DECLARED:
+        unpadded = [tilegen.padded_work(shape, o)[1] for o in tilegen.ORDERS]
+        assert tilegen.padded_work(shape, tilegen.choose_order(shape))[1] <= 2 * min(unpadded)
+
+
+@pytest.mark.parametrize("shape,tile,why", [
+    (tilegen.ShapeDecl("r12", (8, 12, 20), (12, 10, 24), 12), tilegen.Tile(1, 1, 2, 12, 8, 4, 1),
+     "power of two"),
+    (HAND[0], tilegen.Tile(3, 1, 2, 12, 8, 4, 1), "divide 16"),
+    (HAND[0], tilegen.Tile(1, 1, 2, 12, 3, 1, 1), "IC must divide"),
+    (HAND[1], tilegen.Tile(1, 1, 10, 12, 8, 1, 1), "LDS"),
+    (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 3, 1), "KS3"),
+])
+def test_planted_tile_mistakes_are_rejected(shape, tile, why):
+    assert why in tilegen.geometry(shape, (2, 1, 0), tile)["reject"]
+
+
+def test_rule_ranges_cover_everything():
+    for names in (["t1_s1", "mid_half", "mid_all", "wide8x32w8"], ["t1_s2", "mid_all"],
+                  ["t1_s1"]):
+        ranges = tilegen.rule_ranges(names)
+        covered = np.zeros(300, bool)
+        for lo, hi in ranges.values():
+            covered[lo:min(hi, 299) + 1] = True
+        assert covered[1:].all(), names
