@@ -1,0 +1,143 @@
+"""Autotuner of the generated MFMA variant tables: measure every compiled tile of every
+declared shape over a grid of token counts and write the fastest per token range.
+
+    python -m factorized_inference.tilegen --all   # compile every candidate (from kernel-task_amd/)
+    python -m factorized_inference.build_ext
+    python kernel-task_amd/benchmarks/autotune.py --out gpurun_out/tuned.json    # on an MI355X
+    cp gpurun_out/tuned.json kernel-task_amd/csrc/gen/tuned.json
+    python -m factorized_inference.tilegen && python -m factorized_inference.build_ext
+
+Role of the reference's tools/qwen_sweep.py and tools/gen_v3g_tuned.py (a sweep of V3G
+tilings per Qwen shape and token count, reduced to the fastest correct tiling per token
+count, src/factorized_inference/v3g_tuned.py:4-17). Timing: HIP events around a block of
+back-to-back calls, median of three blocks (the harness's stream latency). Every variant's
+output is checked against the shape's default variant before it may win (bitwise equality
+is not expected across tiles: the stage-3 summation order differs).
+
+Token counts measured: 1, 2, 4, 8, 16, 32, 64, 128, 256. The winner at T serves the range
+(previous measured T, T]; 256's winner serves everything above.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from dataclasses import asdict
+from pathlib import Path
+
+os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "0")  # as bench.py
+PACKAGE_ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(PACKAGE_ROOT))
+
+import torch  # noqa: E402
+
+from factorized_inference import TRSpec, make_cores, prepare_optimized, tilegen  # noqa: E402
+
+GRID = (1, 2, 4, 8, 16, 32, 64, 128, 256)
+
+
+def stream_us(fn, calls: int, blocks: int = 3) -> float:
+    out = []
+    for _ in range(blocks):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(calls):
+            fn()
+        e.record()
+        e.synchronize()
+        out.append(s.elapsed_time(e) * 1000.0 / calls)
+    return statistics.median(out)
+
+
+def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
+    dtype = torch.bfloat16 if shape.dtype == "bf16" else torch.float16
+    spec = TRSpec(shape.ins, shape.outs, shape.rank)
+    cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init="uniform")
+    run = prepare_optimized(cores, spec)
+    variants = [(i, v) for i, v in enumerate(run.variants()) if v["kind"] == "mfma"]
+    names = {}
+    cands = tilegen.candidates(shape)
+    for i, v in variants:
+        order, tile = tilegen.parse_variant_name(v["name"])
+        names[i] = next((n for n, t in cands.items() if t == tile), v["name"])
+    measured: dict[int, dict[str, float]] = {}
+    t_end = time.perf_counter() + budget_s
+    for T in GRID:
+        x = torch.randn(T, spec.in_features, device="cuda", dtype=dtype,
+                        generator=torch.Generator(device="cuda").manual_seed(T))
+        ref = run(x).float()
+        scale = ref.abs().max().item()
+        row = {}
+        for i, v in variants:
+            y = run.run_variant(x, i).float()
+            torch.cuda.synchronize()
+            err = (y - ref).abs().max().item()
+            if not (err <= 0.02 * scale + 0.02):  # a tile that disagrees never wins
+                print(f"  {shape.key} T={T} {v['name']}: disagrees ({err:.3e}), skipped",
+                      flush=True)
+                continue
+            fn = lambda i=i: run.run_variant(x, i)  # noqa: E731
+            fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            one = (time.perf_counter() - t0) * 1e6
+            calls = max(5, min(200, int(2e3 / max(one, 1.0))))
+            row[names[i]] = stream_us(fn, calls)
+        measured[T] = row
+        best = min(row, key=row.get)
+        print(f"{shape.key} T={T:4d}: " + "  ".join(
+            f"{n} {us:7.2f}{'*' if n == best else ''}" for n, us in sorted(row.items())),
+            flush=True)
+        if time.perf_counter() > t_end:
+            print(f"  {shape.key}: time budget spent after T={T}", flush=True)
+            break
+    # winners per range (previous T, T]; the last measured T serves everything above
+    ranges = []
+    lo = 1
+    done = sorted(measured)
+    for k, T in enumerate(done):
+        row = measured[T]
+        best = min(row, key=row.get)
+        hi = (1 << 30) if k == len(done) - 1 else T
+        if ranges and ranges[-1]["name"] == best:
+            ranges[-1]["t_max"] = hi
+        else:
+            ranges.append({"name": best, "t_min": lo, "t_max": hi})
+        lo = T + 1
+    order = tilegen.choose_order(shape)
+    for r in ranges:
+        r["tile"] = asdict(cands[r["name"]])
+    return {"order": list(order), "device": torch.cuda.get_device_name(0),
+            "measured_us": {str(T): row for T, row in measured.items()}, "ranges": ranges}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--out", type=Path, required=True)
+    ap.add_argument("--shapes", default="", help="comma-separated shape keys (default: all)")
+    ap.add_argument("--seconds-per-shape", type=float, default=60.0)
+    args = ap.parse_args()
+    if not torch.cuda.is_available():
+        print("autotune.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    wanted = set(filter(None, args.shapes.split(",")))
+    result = json.loads(args.out.read_text()) if args.out.exists() else {}
+    with torch.inference_mode():
+        for shape in tilegen.DECLARED:
+            if wanted and shape.key not in wanted:
+                continue
+            result[shape.key] = tune_shape(shape, args.seconds_per_shape)
+            args.out.parent.mkdir(parents=True, exist_ok=True)
+            args.out.write_text(json.dumps(result, indent=1, sort_keys=True) + "\n")
+    print(f"wrote {args.out}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

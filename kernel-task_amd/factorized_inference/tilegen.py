@@ -26,6 +26,7 @@ kernel's.
 from __future__ import annotations
 
 import json
+import re
 from dataclasses import asdict, dataclass, field
 from pathlib import Path
 
@@ -39,6 +40,7 @@ LDS_LIMIT = 160 * 1024
 # registers a wave may give to the register-resident core slices (4 waves: one wave per
 # SIMD; 8 waves: two per SIMD, half the register file each)
 WIDE_VGPR_BUDGET = {4: 136, 8: 128}
+WIDE_VGPR_RELAXED = {4: 168, 8: 152}  # offered only when no tile fits the budget above
 ORDERS = ((0, 1, 2), (1, 2, 0), (2, 0, 1), (0, 2, 1), (1, 0, 2), (2, 1, 0))
 
 
@@ -209,7 +211,8 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (c.xrow or c.IN % 8 == 0, "scatter loader reads x rows in 8-element vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= sz["Ub"] * 2, "stage-3 reduction does not fit in Ub"),
-        (not wide or g["slice_vgprs"] <= WIDE_VGPR_BUDGET[NW], "register-resident slices too large"),
+        (not wide or g["slice_vgprs"] <= WIDE_VGPR_RELAXED[NW],
+         "register-resident slices too large"),
     ]
     g["reject"] = next((why for ok, why in checks if not ok), "")
     return g
@@ -224,6 +227,17 @@ def _fit(shape, order, make, ics) -> Tile | None:
     for ic in ics:
         t = make(ic)
         if t is not None and not geometry(shape, order, t)["reject"]:
+            return t
+    return None
+
+
+def _fit_budget(shape, order, make, ics, budget: int) -> Tile | None:
+    """The first register-resident tile make(ic) over ics whose core slices take at most
+    `budget` registers and that passes every other check of the kernel."""
+    for ic in ics:
+        t = make(ic)
+        g = geometry(shape, order, t)
+        if g["reject"] in ("", "register-resident slices too large") and g["slice_vgprs"] <= budget:
             return t
     return None
 
@@ -252,20 +266,44 @@ def candidates(shape: ShapeDecl, order: tuple | None = None) -> dict[str, Tile]:
     add("mid_half", lambda ic: Tile(1, 1, half, LC, ic, 1, 2), ics)
     add("mid_all", lambda ic: Tile(1, 1, c.oS, LC, ic, 1, 2), ics)
     # many tokens: register-resident core slices, 4 tokens per workgroup, 32x32 stage 2
-    for wide, nw in ((4, 4), (8, 8)):
-        budget = WIDE_VGPR_BUDGET[nw]
-        best = None
+    def wide_tile(wide, nw, budget):
         for sc_max in range(c.oS, 0, -1):
             chunks = cdiv(c.oS, sc_max)
             sc = cdiv(c.oS, chunks)  # balanced chunks
-            t = _fit(shape, order, lambda ic, sc=sc: Tile(4, 1, sc, LC, ic, 2, 1, wide, 32, nw),
-                     [d for d in ics if d <= 2] or ics[-1:])
-            if t is not None and geometry(shape, order, t).get("slice_vgprs", 0) <= budget:
-                best = t
-                break
-        if best is not None and best not in out.values():
-            out[f"wide{wide}x32" + ("w8" if nw == 8 else "")] = best
+            make = lambda ic, sc=sc: Tile(4, 1, sc, LC, ic, 2, 1, wide, 32, nw)  # noqa: E731
+            t = _fit_budget(shape, order, make, [d for d in ics if d <= 2] or ics[-1:], budget)
+            if t is not None:
+                return t
+        return None
+
+    for wide, nw in ((4, 4), (8, 8)):
+        t = wide_tile(wide, nw, WIDE_VGPR_BUDGET[nw])
+        if t is not None and t not in out.values():
+            out[f"wide{wide}x32" + ("w8" if nw == 8 else "")] = t
+    if not any(n.startswith("wide") for n in out):
+        # no register-resident tile within the budget (a long stage-2 K): offer the smallest
+        # over-budget one, which may spill a few registers; the autotuner decides
+        for wide, nw in ((4, 4), (8, 8)):
+            t = wide_tile(wide, nw, WIDE_VGPR_RELAXED[nw])
+            if t is not None and t not in out.values():
+                out[f"wide{wide}x32" + ("w8" if nw == 8 else "") + "_relaxed"] = t
     return out
+
+
+_VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?|(_w8))?<(\d)(\d)(\d),"
+                           r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
+
+
+def parse_variant_name(name: str) -> tuple[tuple, Tile]:
+    """(chain order, tile) of an MFMA variant from its name in the plan (trk_variant_info)."""
+    m = _VARIANT_NAME.fullmatch(name)
+    if not m:
+        raise ValueError(f"not an MFMA variant name: {name!r}")
+    wide = int(m.group(1) or 0)
+    order = tuple(int(m.group(i)) for i in (5, 6, 7))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(8, 15))
+    return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
+                       8 if (m.group(3) or m.group(4)) else 4)
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
@@ -273,6 +311,9 @@ def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
     ranges = {}
     pick = lambda *opts: next((o for o in opts if o in names), None)  # noqa: E731
     t1 = ("t1_s2", "t1_s1", "t1_s1_w8")
+    # an over-budget register-resident tile takes its family's place
+    original = {n.removesuffix("_relaxed"): n for n in names}
+    names = list(original)
     for name, lo, hi in ((pick(*t1, "mid_half", "mid_all", "wide4x32", "wide8x32w8"), 1, 1),
                          (pick("mid_half", "mid_all", "wide4x32", "wide8x32w8", *t1), 2, 16),
                          (pick("mid_all", "mid_half", "wide4x32", "wide8x32w8", *t1), 17, 64),
@@ -280,6 +321,7 @@ def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
                           1 << 30)):
         if name is None:
             continue
+        name = original[name]
         if name in ranges:  # extend the range a tile already serves
             ranges[name] = (min(ranges[name][0], lo), max(ranges[name][1], hi))
         else:
@@ -291,11 +333,13 @@ def load_tuned() -> dict:
     return json.loads(TUNED.read_text()) if TUNED.exists() else {}
 
 
-def table(shape: ShapeDecl, tuned: dict | None = None) -> tuple[tuple, list[tuple[str, Tile, int, int]]]:
+def table(shape: ShapeDecl, tuned: dict | None = None,
+          all_candidates: bool = False) -> tuple[tuple, list[tuple[str, Tile, int, int]]]:
     """(order, [(name, tile, t_min, t_max)]) for one shape: the tuned winners when the shape
-    has measurements, else every candidate with the rule's ranges (0, 0: index only)."""
+    has measurements, else every candidate with the rule's ranges (0, 0: index only).
+    all_candidates=True ignores the measurements (the autotuner's input)."""
     tuned = load_tuned() if tuned is None else tuned
-    entry = tuned.get(shape.key)
+    entry = None if all_candidates else tuned.get(shape.key)
     if entry:
         order = tuple(entry["order"])
         rows = [(r["name"], Tile(**r["tile"]), r["t_min"], r["t_max"]) for r in entry["ranges"]]
@@ -314,12 +358,13 @@ def _fn_name(shape: ShapeDecl) -> str:
     return "mfma_register_gen_" + shape.key
 
 
-def emit(shape: ShapeDecl, tuned: dict | None = None) -> str:
-    order, rows = table(shape, tuned)
+def emit(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = False) -> str:
+    tuned = load_tuned() if tuned is None else tuned
+    order, rows = table(shape, tuned, all_candidates)
     i, o = shape.ins, shape.outs
     tuned_note = ("token ranges measured by kernel-task_amd/benchmarks/autotune.py"
-                  if (load_tuned() if tuned is None else tuned).get(shape.key)
-                  else "token ranges by rule (not yet tuned)")
+                  if tuned.get(shape.key) and not all_candidates
+                  else "every candidate, token ranges by rule (not tuned)")
     lines = [
         "// Generated by kernel-task_amd/factorized_inference/tilegen.py; do not edit.",
         f"// {shape.name}: ({i[0]},{i[1]},{i[2]}) -> ({o[0]},{o[1]},{o[2]}), rank "
@@ -368,15 +413,17 @@ def emit_index(shapes: list[ShapeDecl]) -> str:
     return "\n".join(lines)
 
 
-def write_all(shapes: list[ShapeDecl] = DECLARED, out_dir: Path = GEN_DIR) -> list[Path]:
+def write_all(shapes: list[ShapeDecl] = DECLARED, out_dir: Path = GEN_DIR,
+              all_candidates: bool = False) -> list[Path]:
     """Write one translation unit per shape plus the index; stale generated units are
-    removed. Returns the written sources."""
+    removed. Returns the written sources. all_candidates=True compiles every candidate with
+    rule ranges (for the autotuner) instead of the tuned winners."""
     out_dir.mkdir(parents=True, exist_ok=True)
     tuned = load_tuned()
     written = []
     for s in shapes:
         p = out_dir / f"trk_gen_{s.key}.hip"
-        text = emit(s, tuned)
+        text = emit(s, tuned, all_candidates)
         if not p.exists() or p.read_text() != text:
             p.write_text(text)
         written.append(p)
@@ -407,5 +454,7 @@ def describe(shapes: list[ShapeDecl] = DECLARED) -> list[dict]:
 
 
 if __name__ == "__main__":
-    for path in write_all():
+    import sys
+
+    for path in write_all(all_candidates="--all" in sys.argv[1:]):
         print(path)

@@ -11,15 +11,11 @@
 """
 from __future__ import annotations
 
-import re
-
 import numpy as np
 import pytest
 
 from factorized_inference import _lib, tilegen
 
-NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?|(_w8))?<(\d)(\d)(\d),"
-                  r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 HAND = [
     tilegen.ShapeDecl("r8", (8, 12, 20), (12, 10, 24), 8, "f16"),
     tilegen.ShapeDecl("r16", (8, 12, 20), (12, 10, 24), 16, "f16"),
@@ -30,14 +26,18 @@ DT = {"f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16}
 
 
 def parse(name: str):
-    m = NAME.fullmatch(name)
-    assert m, name
-    wide = int(m.group(1) or 0)
-    order = tuple(int(m.group(i)) for i in (5, 6, 7))
-    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(8, 15))
-    tile = tilegen.Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
-                        8 if (m.group(3) or m.group(4)) else 4)
-    return order, tile
+    return tilegen.parse_variant_name(name)
+
+
+def test_variant_names_parse_back_to_their_tiles():
+    assert parse("ring3_mfma<210,1,1,2,12,8,4,1>") == ((2, 1, 0), tilegen.Tile(1, 1, 2, 12, 8, 4, 1))
+    assert parse("ring3_mfma_w8<210,1,1,1,12,4,8,1>") == (
+        (2, 1, 0), tilegen.Tile(1, 1, 1, 12, 4, 8, 1, 0, 16, 8))
+    assert parse("ring3_mfma_wide8x32w8<012,4,1,28,32,4,1,2>") == (
+        (0, 1, 2), tilegen.Tile(4, 1, 28, 32, 4, 1, 2, 8, 32, 8))
+    assert parse("ring3_mfma_wide2<210,4,1,8,16,1,2,1>")[1].MF2 == 16
+    with pytest.raises(ValueError):
+        parse("ring3_generic<012,rc=8>")
 
 
 @pytest.mark.parametrize("shape", HAND + tilegen.DECLARED, ids=lambda s: s.key)
