@@ -35,7 +35,7 @@ Plan *as_plan(trk_plan *plan) { return reinterpret_cast<Plan *>(plan); }
 void grid_of(const Plan &p, const Variant &v, int tokens, int grid[3]) {
     const Chain &c = p.chains[v.chain];
     if (v.kind == TRK_KERNEL_GENERIC) {
-        grid[0] = c.oF;
+        grid[0] = c.oF * ((c.oS + v.tile[2] - 1) / v.tile[2]);
         grid[1] = std::max(1, std::min(tokens, 65535));
         grid[2] = 1;
     } else {
@@ -152,9 +152,15 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
             best_flops = fl;
         }
     }
+    // Variant 0: one workgroup per (token, first-core output) owns all second-core outputs;
+    // it serves every token count no other variant claims. Variant 1, when the shape has
+    // few first-core outputs: the second-core outputs are split over workgroups as well
+    // (stage 1 recomputed per split, the rank^3 stage divided), for token counts too small
+    // to fill the GPU with variant 0's workgroups.
     Variant &g = p->variants[0];
     g.chain = plan_chain(p, kOrders[best]);
-    const int st = generic_configure(*p, g.chain, &g);
+    const Chain &gc = p->chains[g.chain];
+    int st = generic_configure(*p, g.chain, gc.oS, &g);
     if (st != TRK_OK) {
         delete p;
         return st;
@@ -162,6 +168,18 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     g.t_min = 1;
     g.t_max = 1 << 30;
     p->nvariants = 1;
+    constexpr int kFillGroups = 512;  // two workgroups per CU
+    const int nsg = std::min(gc.oS, std::max(1, kFillGroups / gc.oF));
+    const int sg = (gc.oS + nsg - 1) / nsg;
+    if (sg < gc.oS) {
+        Variant &spread = p->variants[1];
+        if (generic_configure(*p, g.chain, sg, &spread) == TRK_OK) {
+            spread.t_min = 1;
+            spread.t_max = std::max(1, (kFillGroups - 1) / gc.oF);  // variant 0 below 512 groups
+            p->nvariants = 2;
+        }
+        g_error[0] = '\0';
+    }
     mfma_register_lds(p);
     mfma_register_wide(p);
     mfma_register_generated(p);

@@ -26,11 +26,14 @@ constexpr int kLdsBudget = 64 * 1024;
 
 struct GenericArgs {
     int T, in_features, out_features;
-    int R, RC;
+    int R, RC, SG, nSG;
     int nF, nS, nL, oF, oS, oL, KF, K2;
     int sxF, sxS, sxL, syF, syS, syL;
 };
 
+// Workgroup (f, sg) of token t owns y[t, f, s, :] for the SG second-core digits
+// s in [sg*SG, sg*SG + SG). Stage 1 (the cheapest stage) is recomputed by every sg of an f;
+// stage 2, the rank^3 stage, is split over them without overlap.
 template <int DT>
 __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
     const typename Elem<DT>::T *__restrict__ x, const typename Elem<DT>::T *__restrict__ Fk,
@@ -38,13 +41,15 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
     void *y, GenericArgs a, const void *aux, int epi_mode) {  // aux may equal y
     using E = Elem<DT>;
     extern __shared__ float lds[];
-    const int R = a.R, RC = a.RC;
+    const int R = a.R, RC = a.RC, SG = a.SG;
     float *U = lds;                       // [RC][nS][R]
-    float *V = U + RC * a.nS * R;         // [RC][oS][R]
-    float *Y = V + RC * a.oS * R;         // [oS][oL]
-    const int f = blockIdx.x;
+    float *V = U + RC * a.nS * R;         // [RC][SG][R]
+    float *Y = V + RC * SG * R;           // [SG][oL]
+    const int f = blockIdx.x / a.nSG;
+    const int s0 = (blockIdx.x % a.nSG) * SG;
+    const int SGv = min(SG, a.oS - s0);
     const int tid = threadIdx.x;
-    const int nU = a.nS * R, nV = a.oS * R, nY = a.oS * a.oL;
+    const int nU = a.nS * R, nV = SGv * R, nY = SGv * a.oL;
 
     for (int t = blockIdx.y; t < a.T; t += gridDim.y) {
         const typename E::T *xt = x + size_t(t) * a.in_features;
@@ -69,10 +74,10 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
                     const int r1 = idx / nV;
                     const int s = (idx % nV) / R, r3 = idx % R;
                     const float *u = U + r1 * nU;
-                    const typename E::T *sk = Sk + (size_t(s) * R + r3) * a.K2;
+                    const typename E::T *sk = Sk + (size_t(s0 + s) * R + r3) * a.K2;
                     float acc = 0.0f;
                     for (int k = 0; k < nU; ++k) acc += u[k] * E::to_f32(sk[k]);
-                    V[idx] = acc;
+                    V[(r1 * SG + s) * R + r3] = acc;
                 }
                 __syncthreads();
                 // stage 3: each thread owns its Y entries, so no barrier follows
@@ -81,7 +86,7 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
                     const typename E::T *lk = Lk + ((size_t(iL) * a.oL + l) * R + r1c) * R;
                     float acc = Y[idx];
                     for (int r1 = 0; r1 < rc; ++r1) {
-                        const float *v = V + (r1 * a.oS + s) * R;
+                        const float *v = V + (r1 * SG + s) * R;
                         for (int r3 = 0; r3 < R; ++r3) acc += v[r3] * E::to_f32(lk[r1 * R + r3]);
                     }
                     Y[idx] = acc;
@@ -91,7 +96,7 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
         const size_t yt = size_t(t) * a.out_features + size_t(f) * a.syF;
         for (int idx = tid; idx < nY; idx += kThreads) {
             const int s = idx / a.oL, l = idx % a.oL;
-            const size_t o = yt + s * a.syS + l * a.syL;
+            const size_t o = yt + (s0 + s) * a.syS + l * a.syL;
             epi_put<DT>(y, epi_mode, o, Y[idx], epi_aux<DT>(aux, epi_mode, o));
         }
         __syncthreads();  // U of the next token is written after every thread left stage 2
@@ -100,32 +105,33 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
 
 __global__ void ring3_empty_kernel() {}
 
-int lds_bytes(const Chain &c, int rc) {
-    return 4 * (rc * c.R * (c.nS + c.oS) + c.oS * c.oL);
+int lds_bytes(const Chain &c, int rc, int sg) {
+    return 4 * (rc * c.R * (c.nS + sg) + sg * c.oL);
 }
 
 }  // namespace
 
-int generic_configure(const Plan &plan, int chain, Variant *v) {
+int generic_configure(const Plan &plan, int chain, int sg, Variant *v) {
     const Chain &c = plan.chains[chain];
+    if (sg < 1 || sg > c.oS) return set_error(TRK_ERR_INVALID, "generic kernel: bad s-chunk %d", sg);
     int rc = c.R;
-    while (rc > 1 && lds_bytes(c, rc) > kLdsBudget) rc = (rc + 1) / 2;
-    if (lds_bytes(c, rc) > kLdsBudget)
+    while (rc > 1 && lds_bytes(c, rc, sg) > kLdsBudget) rc = (rc + 1) / 2;
+    if (lds_bytes(c, rc, sg) > kLdsBudget)
         return set_error(TRK_ERR_UNSUPPORTED,
                          "generic kernel: second/last core outputs too large for LDS");
     v->kind = TRK_KERNEL_GENERIC;
     v->chain = chain;
     v->tile[0] = 1;
     v->tile[1] = 1;
-    v->tile[2] = c.oS;
+    v->tile[2] = sg;
     v->tile[3] = c.oL;
     v->tile[4] = rc;
     v->block = kThreads;
-    v->lds_bytes = lds_bytes(c, rc);
+    v->lds_bytes = lds_bytes(c, rc, sg);
     v->launch = launch_generic;
     static const char kNames[] = "012";
-    snprintf(v->name, sizeof(v->name), "ring3_generic<%c%c%c,rc=%d>", kNames[c.order[0]],
-             kNames[c.order[1]], kNames[c.order[2]], rc);
+    snprintf(v->name, sizeof(v->name), "ring3_generic<%c%c%c,rc=%d,sc=%d>", kNames[c.order[0]],
+             kNames[c.order[1]], kNames[c.order[2]], rc, sg);
     return TRK_OK;
 }
 
@@ -138,6 +144,8 @@ int launch_generic(const Plan &plan, const Variant &v, const void *packed, const
     a.out_features = plan.out_features;
     a.R = c.R;
     a.RC = v.tile[4];
+    a.SG = v.tile[2];
+    a.nSG = (c.oS + a.SG - 1) / a.SG;
     a.nF = c.nF;
     a.nS = c.nS;
     a.nL = c.nL;
@@ -153,7 +161,7 @@ int launch_generic(const Plan &plan, const Variant &v, const void *packed, const
     a.syS = c.syS;
     a.syL = c.syL;
     const char *base = static_cast<const char *>(packed);
-    const dim3 grid(c.oF, std::max(1, std::min(tokens, 65535)));
+    const dim3 grid(c.oF * a.nSG, std::max(1, std::min(tokens, 65535)));
     switch (plan.dtype) {
 #define TRK_LAUNCH_GENERIC(DT)                                                                 \
     case DT: {                                                                                 \

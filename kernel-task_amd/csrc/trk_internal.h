@@ -82,7 +82,8 @@ int plan_chain(Plan *plan, const int order[3]);
 // kernels and their launchers
 int launch_pack(const Plan &plan, const void *g1, const void *g2, const void *g3, void *packed,
                 hipStream_t stream);                                   // trk_pack.hip
-int generic_configure(const Plan &plan, int chain, Variant *v);       // trk_generic.hip
+// generic kernel variant of `chain` whose workgroups own `sg` second-core outputs each
+int generic_configure(const Plan &plan, int chain, int sg, Variant *v);  // trk_generic.hip
 int launch_generic(const Plan &plan, const Variant &v, const void *packed, const void *x,
                    void *y, int tokens, Epi epi, hipStream_t stream);  // trk_generic.hip
 int launch_empty(hipStream_t stream);                                  // trk_generic.hip

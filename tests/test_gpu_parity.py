@@ -174,7 +174,10 @@ def test_odd_shapes(ins, outs, rank, dtype):
     run = prepare_optimized(cores, spec)
     for tokens in (1, 3):
         x = gpu_x(spec, tokens, 50 + tokens, dtype)
-        check_result(run(x), oracle_y(x, cores, spec), dtype)
+        expected = oracle_y(x, cores, spec)
+        check_result(run(x), expected, dtype)
+        for variant, info in enumerate(run.variants(tokens)):  # e.g. both generic splits
+            check_result(run.run_variant(x, variant), expected, dtype)
 
 
 # ---- the committed golden vectors (tests/golden/oracle_vectors.npz) -------------------------
