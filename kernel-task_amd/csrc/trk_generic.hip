@@ -2,17 +2,17 @@
 //
 // Role of the reference's generic WMMA kernel (tr_ring.cu:104-338), own design: instead of
 // splitting the ring into pieces over workgroups and reducing them through an fp32
-// workspace with atomics and a last-block finish, one workgroup owns one token and one
-// output digit f of the first core in the contraction chain, and loops over every piece
-// (iL, r1) itself. No workspace, counter or second pass exists, the result is
-// deterministic, and calls share no state.
+// workspace with atomics and a last-block finish, one workgroup owns one token, one output
+// digit f of the first core in the contraction chain and a chunk of the second core's
+// outputs s, and loops over every piece (iL, r1) itself. No workspace, counter or second
+// pass exists, the result is deterministic, and calls share no state.
 //
-// Per workgroup (f, t), for every last-core input digit iL and ring-link chunk r1:
+// Per workgroup (f, s-chunk, t), for every last-core input digit iL and ring-link chunk r1:
 //   stage 1  U[r1][iS][r2] = sum_iF      x[t, iF, iS, iL] * Fc[r1][f][iF][r2]
 //   stage 2  V[r1][s][r3]  = sum_{iS,r2} U[r1][iS][r2]     * Sc[r2][s][iS][r3]
 //   stage 3  Y[s][l]      += sum_{r1,r3} V[r1][s][r3]      * Lc[r3][l][iL][r1]
-// with U, V and Y in LDS (fp32) and the cores read from the packed buffer (L2-resident).
-// This is the fallback for shapes without a compiled MFMA variant; it runs on VALU FMAs.
+// with the workgroup's core slices, U, V and Y in LDS. This is the fallback for shapes
+// without a compiled MFMA variant; it runs on VALU FMAs.
 #include <algorithm>
 
 #include "trk_internal.h"
@@ -22,73 +22,144 @@ namespace trk {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLdsBudget = 64 * 1024;
+constexpr int kLdsPreferred = 64 * 1024;  // two workgroups per CU
+constexpr int kLdsMax = 160 * 1024;
 
 struct GenericArgs {
     int T, in_features, out_features;
     int R, RC, SG, nSG;
     int nF, nS, nL, oF, oS, oL, KF, K2;
     int sxF, sxS, sxL, syF, syS, syL;
+    int pF, p2, pL;                               // LDS row pitches, in elements of the dtype
+    int offSs, offLs, offU, offV, offY, offX;     // LDS byte offsets (Fs at 0)
 };
 
+// Row pitch (elements) of an LDS row of n elements of `esize` bytes: an odd number of 4-byte
+// words, so the rows that consecutive threads read start in different banks.
+int odd_pitch(int n, int esize) {
+    int words = (n * esize + 3) / 4;
+    if (words % 2 == 0) ++words;
+    return words * 4 / esize;
+}
+
+int align16(int v) { return (v + 15) & ~15; }
+
+// LDS layout of one workgroup for s-chunk sg and ring-link chunk rc; returns the bytes.
+int layout(const Chain &c, int esize, int sg, int rc, GenericArgs *a) {
+    const int R = c.R;
+    a->pF = odd_pitch(c.nF, esize);
+    a->p2 = odd_pitch(c.nS * R, esize);
+    a->pL = odd_pitch(R * R, esize);
+    int off = align16(R * R * a->pF * esize);     // Fs[R*R][pF]
+    a->offSs = off;
+    off += align16(sg * R * a->p2 * esize);        // Ss[sg*R][p2]
+    a->offLs = off;
+    off += align16(c.oL * a->pL * esize);          // Ls[oL][pL]
+    a->offU = off;
+    off += align16(rc * c.nS * R * 4);             // U[rc][nS][R]
+    a->offV = off;
+    off += align16(rc * sg * R * 4);               // V[rc][sg][R]
+    a->offY = off;
+    off += align16(sg * c.oL * 4);                 // Y[sg][oL]
+    a->offX = off;
+    off += align16(c.nF * c.nS * c.nL * esize);    // Xs[in]: the token's row of x
+    return off;
+}
+
+// sum_k u[k] * w[k] for k < n: 8 independent partial sums, so that the LDS reads of 8 terms
+// are in flight together (a single accumulator chain waits out the LDS latency per term)
+template <class E>
+__device__ inline float dot8(const float *u, const typename E::T *w, int n) {
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int k = 0;
+    for (; k + 8 <= n; k += 8)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] += u[k + q] * E::to_f32(w[k + q]);
+    for (; k < n; ++k) acc[0] += u[k] * E::to_f32(w[k]);
+    return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+
 // Workgroup (f, sg) of token t owns y[t, f, s, :] for the SG second-core digits
-// s in [sg*SG, sg*SG + SG). Stage 1 (the cheapest stage) is recomputed by every sg of an f;
-// stage 2, the rank^3 stage, is split over them without overlap.
+// s in [sg*SG, sg*SG + SG). Its first- and second-core slices are staged in LDS once, the
+// last core one input digit iL at a time; stage 1 (the cheapest stage) is recomputed by every
+// sg of an f, stage 2 (the rank^3 stage) is split over them without overlap. Every LDS row
+// that consecutive threads read has an odd word pitch.
 template <int DT>
 __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
     const typename Elem<DT>::T *__restrict__ x, const typename Elem<DT>::T *__restrict__ Fk,
     const typename Elem<DT>::T *__restrict__ Sk, const typename Elem<DT>::T *__restrict__ Lk,
     void *y, GenericArgs a, const void *aux, int epi_mode) {  // aux may equal y
     using E = Elem<DT>;
-    extern __shared__ float lds[];
-    const int R = a.R, RC = a.RC, SG = a.SG;
-    float *U = lds;                       // [RC][nS][R]
-    float *V = U + RC * a.nS * R;         // [RC][SG][R]
-    float *Y = V + RC * SG * R;           // [SG][oL]
+    using ET = typename E::T;
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int R = a.R, RC = a.RC, SG = a.SG, R2 = R * R;
+    ET *Fs = reinterpret_cast<ET *>(lds);                // [R*R][pF]: row r1*R + r2
+    ET *Ss = reinterpret_cast<ET *>(lds + a.offSs);      // [SG*R][p2]: row s*R + r3
+    ET *Ls = reinterpret_cast<ET *>(lds + a.offLs);      // [oL][pL]: row l, column r1*R + r3
+    float *U = reinterpret_cast<float *>(lds + a.offU);  // [RC][nS][R]
+    float *V = reinterpret_cast<float *>(lds + a.offV);  // [RC][SG][R]
+    float *Y = reinterpret_cast<float *>(lds + a.offY);  // [SG][oL]
+    ET *Xs = reinterpret_cast<ET *>(lds + a.offX);       // [in]: the token's row of x
     const int f = blockIdx.x / a.nSG;
     const int s0 = (blockIdx.x % a.nSG) * SG;
     const int SGv = min(SG, a.oS - s0);
     const int tid = threadIdx.x;
     const int nU = a.nS * R, nV = SGv * R, nY = SGv * a.oL;
 
+    // the first- and second-core slices of this workgroup, read row by row (coalesced)
+    for (int i = tid; i < R2 * a.nF; i += kThreads) {
+        const int row = i / a.nF, iF = i % a.nF;
+        Fs[row * a.pF + iF] = Fk[(size_t(f) * R2 + row) * a.KF + iF];
+    }
+    for (int i = tid; i < SGv * R * nU; i += kThreads) {
+        const int row = i / nU, k = i % nU;
+        Ss[row * a.p2 + k] = Sk[(size_t(s0) * R + row) * a.K2 + k];
+    }
+
     for (int t = blockIdx.y; t < a.T; t += gridDim.y) {
-        const typename E::T *xt = x + size_t(t) * a.in_features;
+        // the previous token's stage 1 is done with Xs: its last iL passed two barriers since
+        const ET *xt = x + size_t(t) * a.in_features;
+        for (int i = tid; i < a.in_features; i += kThreads) Xs[i] = xt[i];
         for (int i = tid; i < nY; i += kThreads) Y[i] = 0.0f;
         for (int iL = 0; iL < a.nL; ++iL) {
+            __syncthreads();  // the previous iL's stage 3 is done with Ls
+            const ET *lk = Lk + size_t(iL) * a.oL * R2;
+            for (int i = tid; i < a.oL * R2; i += kThreads) Ls[(i / R2) * a.pL + i % R2] = lk[i];
             for (int r1c = 0; r1c < R; r1c += RC) {
                 const int rc = min(RC, R - r1c);
-                // stage 1 (U was last read by stage 2 of the previous step, before a barrier)
+                __syncthreads();  // Ls (and Fs, Ss) written; stage 2 of the last chunk read U
+                // stage 1: U[r1][iS][r2] = sum_iF x[iF, iS, iL] Fc[r1][f][iF][r2]
                 for (int idx = tid; idx < rc * nU; idx += kThreads) {
                     const int r1 = r1c + idx / nU;
                     const int iS = (idx % nU) / R, r2 = idx % R;
-                    const typename E::T *fk = Fk + ((size_t(f) * R + r1) * R + r2) * a.KF;
-                    const typename E::T *xs = xt + iS * a.sxS + iL * a.sxL;
-                    float acc = 0.0f;
-                    for (int iF = 0; iF < a.nF; ++iF)
-                        acc += E::to_f32(xs[iF * a.sxF]) * E::to_f32(fk[iF]);
-                    U[idx] = acc;
+                    const ET *fs = Fs + (r1 * R + r2) * a.pF;
+                    const ET *xs = Xs + iS * a.sxS + iL * a.sxL;
+                    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    int iF = 0;
+                    for (; iF + 4 <= a.nF; iF += 4)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            acc[q] += E::to_f32(xs[(iF + q) * a.sxF]) * E::to_f32(fs[iF + q]);
+                    for (; iF < a.nF; ++iF) acc[0] += E::to_f32(xs[iF * a.sxF]) * E::to_f32(fs[iF]);
+                    U[idx] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
                 }
                 __syncthreads();
-                // stage 2 (V was last read by stage 3 of the previous step, before the barrier above)
+                // stage 2: V[r1][s][r3] = sum_{iS,r2} U[r1][iS][r2] Sc[r2][s][iS][r3]
                 for (int idx = tid; idx < rc * nV; idx += kThreads) {
-                    const int r1 = idx / nV;
-                    const int s = (idx % nV) / R, r3 = idx % R;
+                    const int r1 = idx / nV, sr = idx % nV;  // sr = s*R + r3
                     const float *u = U + r1 * nU;
-                    const typename E::T *sk = Sk + (size_t(s0 + s) * R + r3) * a.K2;
-                    float acc = 0.0f;
-                    for (int k = 0; k < nU; ++k) acc += u[k] * E::to_f32(sk[k]);
-                    V[(r1 * SG + s) * R + r3] = acc;
+                    const ET *ss = Ss + sr * a.p2;
+                    V[r1 * SG * R + sr] = dot8<E>(u, ss, nU);
                 }
                 __syncthreads();
-                // stage 3: each thread owns its Y entries, so no barrier follows
+                // stage 3: Y[s][l] += sum_{r1,r3} V[r1][s][r3] Lc[r3][l][iL][r1]; each thread
+                // owns its Y entries
                 for (int idx = tid; idx < nY; idx += kThreads) {
                     const int s = idx / a.oL, l = idx % a.oL;
-                    const typename E::T *lk = Lk + ((size_t(iL) * a.oL + l) * R + r1c) * R;
+                    const ET *ls = Ls + l * a.pL + r1c * R;
                     float acc = Y[idx];
-                    for (int r1 = 0; r1 < rc; ++r1) {
-                        const float *v = V + (r1 * SG + s) * R;
-                        for (int r3 = 0; r3 < R; ++r3) acc += v[r3] * E::to_f32(lk[r1 * R + r3]);
-                    }
+                    for (int r1 = 0; r1 < rc; ++r1)
+                        acc += dot8<E>(V + (r1 * SG + s) * R, ls + r1 * R, R);
                     Y[idx] = acc;
                 }
             }
@@ -99,39 +170,47 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
             const size_t o = yt + (s0 + s) * a.syS + l * a.syL;
             epi_put<DT>(y, epi_mode, o, Y[idx], epi_aux<DT>(aux, epi_mode, o));
         }
-        __syncthreads();  // U of the next token is written after every thread left stage 2
     }
 }
 
 __global__ void ring3_empty_kernel() {}
-
-int lds_bytes(const Chain &c, int rc, int sg) {
-    return 4 * (rc * c.R * (c.nS + sg) + sg * c.oL);
-}
 
 }  // namespace
 
 int generic_configure(const Plan &plan, int chain, int sg, Variant *v) {
     const Chain &c = plan.chains[chain];
     if (sg < 1 || sg > c.oS) return set_error(TRK_ERR_INVALID, "generic kernel: bad s-chunk %d", sg);
-    int rc = c.R;
-    while (rc > 1 && lds_bytes(c, rc, sg) > kLdsBudget) rc = (rc + 1) / 2;
-    if (lds_bytes(c, rc, sg) > kLdsBudget)
-        return set_error(TRK_ERR_UNSUPPORTED,
-                         "generic kernel: second/last core outputs too large for LDS");
+    // the largest s-chunk (up to sg) and ring-link chunk that fit two workgroups per CU, else
+    // one workgroup per CU
+    GenericArgs a;
+    int best_sg = 0, best_rc = 0, bytes = 0;
+    for (int budget : {kLdsPreferred, kLdsMax}) {
+        for (int s = sg; s >= 1 && !best_sg; --s)
+            for (int rc = c.R; rc >= 1; rc = rc > 1 ? (rc + 1) / 2 : 0) {
+                const int b = layout(c, plan.elem, s, rc, &a);
+                if (b <= budget) {
+                    best_sg = s, best_rc = rc, bytes = b;
+                    break;
+                }
+                if (rc == 1) break;
+            }
+        if (best_sg) break;
+    }
+    if (!best_sg)
+        return set_error(TRK_ERR_UNSUPPORTED, "generic kernel: core slices too large for LDS");
     v->kind = TRK_KERNEL_GENERIC;
     v->chain = chain;
     v->tile[0] = 1;
     v->tile[1] = 1;
-    v->tile[2] = sg;
+    v->tile[2] = best_sg;
     v->tile[3] = c.oL;
-    v->tile[4] = rc;
+    v->tile[4] = best_rc;
     v->block = kThreads;
-    v->lds_bytes = lds_bytes(c, rc, sg);
+    v->lds_bytes = bytes;
     v->launch = launch_generic;
     static const char kNames[] = "012";
     snprintf(v->name, sizeof(v->name), "ring3_generic<%c%c%c,rc=%d,sc=%d>", kNames[c.order[0]],
-             kNames[c.order[1]], kNames[c.order[2]], rc, sg);
+             kNames[c.order[1]], kNames[c.order[2]], best_rc, best_sg);
     return TRK_OK;
 }
 
@@ -160,13 +239,21 @@ int launch_generic(const Plan &plan, const Variant &v, const void *packed, const
     a.syF = c.syF;
     a.syS = c.syS;
     a.syL = c.syL;
+    const int bytes = layout(c, plan.elem, a.SG, a.RC, &a);
+    if (bytes != v.lds_bytes) return set_error(TRK_ERR_INVALID, "generic kernel: LDS layout mismatch");
     const char *base = static_cast<const char *>(packed);
     const dim3 grid(c.oF * a.nSG, std::max(1, std::min(tokens, 65535)));
     switch (plan.dtype) {
 #define TRK_LAUNCH_GENERIC(DT)                                                                 \
     case DT: {                                                                                 \
         using T = Elem<DT>::T;                                                                 \
-        hipLaunchKernelGGL(ring3_generic_kernel<DT>, grid, dim3(kThreads), v.lds_bytes, stream, \
+        if (bytes > 64 * 1024) {                                                               \
+            const hipError_t err = hipFuncSetAttribute(                                        \
+                reinterpret_cast<const void *>(ring3_generic_kernel<DT>),                      \
+                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                            \
+            if (err != hipSuccess) return check_hip(err, "trk_forward: generic LDS size");     \
+        }                                                                                      \
+        hipLaunchKernelGGL(ring3_generic_kernel<DT>, grid, dim3(kThreads), bytes, stream,     \
                            static_cast<const T *>(x), reinterpret_cast<const T *>(base + c.offF), \
                            reinterpret_cast<const T *>(base + c.offS),                         \
                            reinterpret_cast<const T *>(base + c.offL), y, a, epi.aux, epi.mode); \
