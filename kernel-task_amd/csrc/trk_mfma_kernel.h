@@ -869,21 +869,32 @@ int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const vo
     using E = typename Ops<C.dt>::E;
     const Chain &c = plan.chains[v.chain];
     const char *base = static_cast<const char *>(packed);
-    const dim3 grid(G::NFC * G::NSC * G::NLC, (tokens + G::TT - 1) / G::TT);
-    if (grid.y > 65535u)
-        return set_error(TRK_ERR_UNSUPPORTED, "trk_forward: %d tokens exceed one launch of %s",
-                         tokens, v.name);
-    const E *xe = static_cast<const E *>(x);
     const E *fk = reinterpret_cast<const E *>(base + c.offF);
     const E *sk = reinterpret_cast<const E *>(base + c.offS);
     const E *lk = reinterpret_cast<const E *>(base + c.offL);
-    if (epi.mode == TRK_EPI_STORE)
-        hipLaunchKernelGGL((ring3_mfma_kernel<C, false>), grid, dim3(G::NT), 0, stream, xe, fk, sk,
-                           lk, y, tokens, epi.mode, epi.aux);
-    else
-        hipLaunchKernelGGL((ring3_mfma_kernel<C, true>), grid, dim3(G::NT), 0, stream, xe, fk, sk,
-                           lk, y, tokens, epi.mode, epi.aux);
-    return check_hip(hipGetLastError(), "trk_forward: MFMA kernel launch");
+    // one launch covers at most 65535 token tiles (the grid's y limit); more tokens go in
+    // consecutive launches on the same stream, each on its own rows of x, y and aux
+    constexpr int kMaxTiles = 65535;
+    const int per_launch = kMaxTiles * G::TT;
+    const size_t y_elem = (epi.mode & kEpiKindMask) == TRK_EPI_F32 ? 4 : sizeof(E);
+    const size_t aux_elem = (epi.mode & kAuxF32) ? 4 : sizeof(E);
+    for (int t0 = 0; t0 < tokens; t0 += per_launch) {
+        const int n = tokens - t0 < per_launch ? tokens - t0 : per_launch;
+        const dim3 grid(G::NFC * G::NSC * G::NLC, (n + G::TT - 1) / G::TT);
+        const E *xe = static_cast<const E *>(x) + size_t(t0) * G::IN;
+        void *yc = static_cast<char *>(y) + size_t(t0) * G::OUT * y_elem;
+        const void *ac =
+            epi.aux ? static_cast<const char *>(epi.aux) + size_t(t0) * G::OUT * aux_elem : nullptr;
+        if (epi.mode == TRK_EPI_STORE)
+            hipLaunchKernelGGL((ring3_mfma_kernel<C, false>), grid, dim3(G::NT), 0, stream, xe, fk,
+                               sk, lk, yc, n, epi.mode, ac);
+        else
+            hipLaunchKernelGGL((ring3_mfma_kernel<C, true>), grid, dim3(G::NT), 0, stream, xe, fk,
+                               sk, lk, yc, n, epi.mode, ac);
+        const int st = check_hip(hipGetLastError(), "trk_forward: MFMA kernel launch");
+        if (st != TRK_OK) return st;
+    }
+    return TRK_OK;
 }
 
 struct Entry {
