@@ -9,8 +9,10 @@ declared shape over a grid of token counts and write the fastest per token range
 
 Role of the reference's tools/qwen_sweep.py and tools/gen_v3g_tuned.py (a sweep of V3G
 tilings per Qwen shape and token count, reduced to the fastest correct tiling per token
-count, src/factorized_inference/v3g_tuned.py:4-17). Timing: HIP events around a block of
-back-to-back calls, median of three blocks (the harness's stream latency). Every variant's
+count, src/factorized_inference/v3g_tuned.py:4-17). Timing: HIP events around the replay of
+a HIP graph of back-to-back calls of one tile, median of three replays (GPU time per call
+without the host's per-call cost, which would hide the differences between fast tiles at
+small token counts). Every variant's
 output is checked against the shape's default variant before it may win (bitwise equality
 is not expected across tiles: the stage-3 summation order differs).
 
@@ -39,17 +41,30 @@ from factorized_inference import TRSpec, make_cores, prepare_optimized, tilegen 
 GRID = (1, 2, 4, 8, 16, 32, 64, 128, 256)
 
 
-def stream_us(fn, calls: int, blocks: int = 3) -> float:
+def graph_us(fn, calls: int, blocks: int = 3) -> float:
+    """GPU time per call of `calls` back-to-back calls captured in one HIP graph (no host
+    cost in the timed region, so tiles that finish faster than a call's host work still
+    rank correctly), median of `blocks` replays."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
     out = []
     for _ in range(blocks):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         s.record()
-        for _ in range(calls):
-            fn()
+        graph.replay()
         e.record()
         e.synchronize()
         out.append(s.elapsed_time(e) * 1000.0 / calls)
+    del graph
     return statistics.median(out)
 
 
@@ -59,11 +74,12 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
     cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init="uniform")
     run = prepare_optimized(cores, spec)
     variants = [(i, v) for i, v in enumerate(run.variants()) if v["kind"] == "mfma"]
-    names = {}
-    cands = tilegen.candidates(shape)
+    names, tiles = {}, {}
+    cands = tilegen.candidates(shape, extended=True)
     for i, v in variants:
         order, tile = tilegen.parse_variant_name(v["name"])
         names[i] = next((n for n, t in cands.items() if t == tile), v["name"])
+        tiles[names[i]] = tile
     measured: dict[int, dict[str, float]] = {}
     t_end = time.perf_counter() + budget_s
     for T in GRID:
@@ -87,8 +103,8 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
             fn()
             torch.cuda.synchronize()
             one = (time.perf_counter() - t0) * 1e6
-            calls = max(5, min(200, int(2e3 / max(one, 1.0))))
-            row[names[i]] = stream_us(fn, calls)
+            calls = max(5, min(50, int(2e3 / max(one, 1.0))))
+            row[names[i]] = graph_us(fn, calls)
         measured[T] = row
         best = min(row, key=row.get)
         print(f"{shape.key} T={T:4d}: " + "  ".join(
@@ -112,7 +128,7 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
         lo = T + 1
     order = tilegen.choose_order(shape)
     for r in ranges:
-        r["tile"] = asdict(cands[r["name"]])
+        r["tile"] = asdict(tiles[r["name"]])
     return {"order": list(order), "device": torch.cuda.get_device_name(0),
             "measured_us": {str(T): row for T, row in measured.items()}, "ranges": ranges}
 

@@ -181,8 +181,6 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
         }
         g_error[0] = '\0';
     }
-    mfma_register_lds(p);
-    mfma_register_wide(p);
     mfma_register_generated(p);
     *out = reinterpret_cast<trk_plan *>(p);
     return TRK_OK;

@@ -92,12 +92,9 @@ int launch_silu_mul(const float *g, const float *u, void *out, int out_dtype, si
                     hipStream_t stream);
 int launch_add(const void *h, const float *y, void *out, int dtype, size_t n, hipStream_t stream);
 
-// MFMA variants compiled for this plan's shape: appends to plan->variants and returns how
-// many were added (trk_mfma_lds.hip: core slices in LDS; trk_mfma_wide.hip: in registers).
-int mfma_register_lds(Plan *plan);
-int mfma_register_wide(Plan *plan);
-// Generated tables for the declared shapes (csrc/gen/, written by
-// factorized_inference/tilegen.py): appends the matching shape's variants.
+// MFMA variants of the declared shapes (csrc/gen/, one generated translation unit per shape,
+// written by factorized_inference/tilegen.py): appends the variants of the plan's shape and
+// returns how many were added.
 int mfma_register_generated(Plan *plan);
 
 }  // namespace trk

@@ -1,8 +1,8 @@
 #pragma once
 // MFMA (gfx950 matrix core) variants of the fused tensor-ring kernel, fp16 and bf16: the
-// kernel template, its launch and the variant-table helpers. The tables themselves live in
-// trk_mfma_lds.hip (core slices in LDS) and trk_mfma_wide.hip (core slices in registers),
-// two translation units so that each family gets its own compiler flags.
+// kernel template, its launch and the variant-table helpers. The tables themselves are
+// generated per declared shape (csrc/gen/trk_gen_<shape>.hip, written by
+// factorized_inference/tilegen.py), one translation unit per shape.
 //
 // Role of the reference's V3 / V3T / V3G kernels (tr_ring.cu:543-751, :822-1056,
 // csrc/v3g/v3g.cuh:142-431); own design for CDNA4:
@@ -24,9 +24,10 @@
 //   its 4 results as one 8-byte vector in exactly the layout the next stage reads.
 //   Stage 3 accumulates Y in registers over all steps; with fewer Y tiles than waves, its K
 //   range is split over waves and the partial tiles are summed through LDS at the end.
-// * 16x16x32 MFMAs (16x16x16 for a trailing K of 16), wave64, 4 waves per workgroup.
+// * 16x16x32 MFMAs (16x16x16 for a trailing K of 16), wave64, 4 or 8 waves per workgroup;
+//   the register-resident (WIDE) family runs stage 2 on 32x32x16 MFMAs.
 //
-// Variants are compiled for the shapes and token ranges of the table at the end; plans for
+// Variants are compiled for the declared shapes and their tuned token ranges; plans for
 // other shapes use the generic kernel (trk_generic.hip).
 #include <algorithm>
 #include <cstdio>
@@ -913,10 +914,6 @@ constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, in
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
                 TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW};
 }
-constexpr Shape kR8{TRK_DTYPE_F16, 2, 1, 0, 8, 12, 20, 12, 10, 24, 8};
-constexpr Shape kR16{TRK_DTYPE_F16, 2, 1, 0, 8, 12, 20, 12, 10, 24, 16};
-constexpr Shape kUp{TRK_DTYPE_BF16, 0, 1, 2, 16, 16, 16, 16, 28, 32, 8};
-constexpr Shape kDown{TRK_DTYPE_BF16, 2, 1, 0, 16, 28, 32, 16, 16, 16, 16};
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>},
 

@@ -2,9 +2,9 @@
 
     python -m factorized_inference.tilegen            (from kernel-task_amd/; writes csrc/gen/)
 
-The MFMA kernel (csrc/trk_mfma_kernel.h) is compiled per shape and workgroup tile. The
-four BASELINE shapes have hand-tuned tables (csrc/trk_mfma_lds.hip, trk_mfma_wide.hip); every
-shape declared in DECLARED below gets a generated table instead:
+The MFMA kernel (csrc/trk_mfma_kernel.h) is compiled per shape and workgroup tile. Every
+shape declared in DECLARED below (the BASELINE configs and the reference's Qwen3.8-27B
+shapes) gets a generated table:
 
   1. chain order: the order (F, S, L) with the least MFMA work after padding (stage-1 K to
      16, the second core's input mode to 16 rows, stage-2 K to 16, the last core's outputs to
@@ -61,6 +61,7 @@ class ShapeDecl:
     outs: tuple
     rank: int
     dtype: str = "bf16"
+    order: tuple | None = None  # chain order override (default: least padded MFMA work)
 
     @property
     def key(self) -> str:
@@ -101,8 +102,16 @@ QWEN = {
     "o_proj": ((24, 16, 16), (16, 16, 20)),
     "gdn_qkvz": ((20, 16, 16), (16, 32, 32)),
 }
-DECLARED = [ShapeDecl(f"qwen_{name}", ins, outs, rank)
-            for name, (ins, outs) in QWEN.items() for rank in (8, 16)]
+# The BASELINE configs: 1920 -> 2880 at ranks 8 and 16 in fp16 (chain order (G3, G2, G1), whose
+# stage-1 x reads are contiguous in iF), and the Llama-3-8B up/down projections in bf16.
+BASELINE = [
+    ShapeDecl("r8", (8, 12, 20), (12, 10, 24), 8, "f16", (2, 1, 0)),
+    ShapeDecl("r16", (8, 12, 20), (12, 10, 24), 16, "f16", (2, 1, 0)),
+    ShapeDecl("llama_up", (16, 16, 16), (16, 28, 32), 8, "bf16"),
+    ShapeDecl("llama_down", (16, 28, 32), (16, 16, 16), 16, "bf16"),
+]
+DECLARED = BASELINE + [ShapeDecl(f"qwen_{name}", ins, outs, rank)
+                       for name, (ins, outs) in QWEN.items() for rank in (8, 16)]
 
 
 @dataclass
@@ -138,6 +147,8 @@ def padded_work(shape: ShapeDecl, order: tuple) -> tuple[int, int]:
 
 
 def choose_order(shape: ShapeDecl) -> tuple:
+    if shape.order is not None:
+        return tuple(shape.order)
     return min(ORDERS, key=lambda o: padded_work(shape, o))
 
 
@@ -242,8 +253,12 @@ def _fit_budget(shape, order, make, ics, budget: int) -> Tile | None:
     return None
 
 
-def candidates(shape: ShapeDecl, order: tuple | None = None) -> dict[str, Tile]:
-    """Named candidate tiles for one shape (each accepted by the kernel's constraints)."""
+def candidates(shape: ShapeDecl, order: tuple | None = None,
+               extended: bool = False) -> dict[str, Tile]:
+    """Named candidate tiles for one shape (each accepted by the kernel's constraints).
+    extended=True adds tiles with 2, 4 or 8 tokens per workgroup in every family and
+    single-token tiles over the whole last-core input mode (a wider search for the
+    autotuner)."""
     order = order or choose_order(shape)
     c, R = chain_of(shape, order), shape.rank
     ics = _divisors_desc(c.nL)
@@ -280,6 +295,21 @@ def candidates(shape: ShapeDecl, order: tuple | None = None) -> dict[str, Tile]:
         t = wide_tile(wide, nw, WIDE_VGPR_BUDGET[nw])
         if t is not None and t not in out.values():
             out[f"wide{wide}x32" + ("w8" if nw == 8 else "")] = t
+    if extended:
+        add("t1_s1_icall", lambda ic: Tile(1, 1, 1, LC, ic, 4, 1), ics)
+        add("t1_s2_icall", lambda ic: Tile(1, 1, min(2, c.oS), LC, ic, 4, 1), ics)
+        for tt in (2, 4):
+            add(f"mid_half_t{tt}", lambda ic, tt=tt: Tile(tt, 1, half, LC, ic, 1, 2), ics)
+            add(f"mid_all_t{tt}", lambda ic, tt=tt: Tile(tt, 1, c.oS, LC, ic, 1, 2), ics)
+        for wide, nw in ((4, 4), (8, 8)):
+            base = out.get(f"wide{wide}x32" + ("w8" if nw == 8 else ""))
+            if base is None:
+                continue
+            for tt, ks3, nacc in ((8, 2, 1), (4, 1, 2), (8, 1, 2)):
+                add(f"wide{wide}x32{'w8' if nw == 8 else ''}_t{tt}k{ks3}n{nacc}",
+                    lambda ic, tt=tt, ks3=ks3, nacc=nacc, base=base: Tile(
+                        tt, 1, base.SC, LC, ic, ks3, nacc, wide, 32, nw),
+                    [base.IC] + [d for d in ics if d < base.IC])
     if not any(n.startswith("wide") for n in out):
         # no register-resident tile within the budget (a long stage-2 K): offer the smallest
         # over-budget one, which may spill a few registers; the autotuner decides
@@ -333,8 +363,8 @@ def load_tuned() -> dict:
     return json.loads(TUNED.read_text()) if TUNED.exists() else {}
 
 
-def table(shape: ShapeDecl, tuned: dict | None = None,
-          all_candidates: bool = False) -> tuple[tuple, list[tuple[str, Tile, int, int]]]:
+def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = False,
+          extended: bool = False) -> tuple[tuple, list[tuple[str, Tile, int, int]]]:
     """(order, [(name, tile, t_min, t_max)]) for one shape: the tuned winners when the shape
     has measurements, else every candidate with the rule's ranges (0, 0: index only).
     all_candidates=True ignores the measurements (the autotuner's input)."""
@@ -349,7 +379,7 @@ def table(shape: ShapeDecl, tuned: dict | None = None,
                 raise ValueError(f"{shape.key}: tuned tile {name} is rejected: {why}")
         return order, rows
     order = choose_order(shape)
-    cands = candidates(shape, order)
+    cands = candidates(shape, order, extended)
     ranges = rule_ranges(list(cands))
     return order, [(n, t, *ranges.get(n, (0, 0))) for n, t in cands.items()]
 
@@ -358,9 +388,10 @@ def _fn_name(shape: ShapeDecl) -> str:
     return "mfma_register_gen_" + shape.key
 
 
-def emit(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = False) -> str:
+def emit(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = False,
+         extended: bool = False) -> str:
     tuned = load_tuned() if tuned is None else tuned
-    order, rows = table(shape, tuned, all_candidates)
+    order, rows = table(shape, tuned, all_candidates, extended)
     i, o = shape.ins, shape.outs
     tuned_note = ("token ranges measured by kernel-task_amd/benchmarks/autotune.py"
                   if tuned.get(shape.key) and not all_candidates
@@ -414,7 +445,7 @@ def emit_index(shapes: list[ShapeDecl]) -> str:
 
 
 def write_all(shapes: list[ShapeDecl] = DECLARED, out_dir: Path = GEN_DIR,
-              all_candidates: bool = False) -> list[Path]:
+              all_candidates: bool = False, extended: bool = False) -> list[Path]:
     """Write one translation unit per shape plus the index; stale generated units are
     removed. Returns the written sources. all_candidates=True compiles every candidate with
     rule ranges (for the autotuner) instead of the tuned winners."""
@@ -423,7 +454,7 @@ def write_all(shapes: list[ShapeDecl] = DECLARED, out_dir: Path = GEN_DIR,
     written = []
     for s in shapes:
         p = out_dir / f"trk_gen_{s.key}.hip"
-        text = emit(s, tuned, all_candidates)
+        text = emit(s, tuned, all_candidates, extended)
         if not p.exists() or p.read_text() != text:
             p.write_text(text)
         written.append(p)
@@ -456,5 +487,6 @@ def describe(shapes: list[ShapeDecl] = DECLARED) -> list[dict]:
 if __name__ == "__main__":
     import sys
 
-    for path in write_all(all_candidates="--all" in sys.argv[1:]):
+    for path in write_all(all_candidates="--all" in sys.argv[1:],
+                          extended="--extended" in sys.argv[1:]):
         print(path)

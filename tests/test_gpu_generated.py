@@ -1,11 +1,11 @@
 """GPU parity of the generated MFMA variant tables (factorized_inference/tilegen.py).
 
-Every variant compiled for a declared shape (the reference's Qwen3.8-27B layer shapes,
-tools/qwen_shapes.py:20-27, at ranks 8 and 16 in bf16, as tools/qwen_bench.py runs them)
-is checked against the oracle at 1, 5 and 33 tokens, on a subset of the token rows (rows
-are independent, so a full-size launch is checked row-exactly on the rows sampled), with
-bitwise-identical repeated calls; the plan's default selection is checked at every token
-count the autotuner measures.
+Every variant compiled for a declared shape (the BASELINE configs, and the reference's
+Qwen3.8-27B layer shapes, tools/qwen_shapes.py:20-27, at ranks 8 and 16 in bf16, as
+tools/qwen_bench.py runs them) is checked against the oracle at 1, 5 and 33 tokens, on a
+subset of the token rows (rows are independent, so a full-size launch is checked row-exactly
+on the rows sampled), with bitwise-identical repeated calls; the plan's default selection
+is checked at every token count the autotuner measures.
 """
 from __future__ import annotations
 
@@ -54,7 +54,8 @@ def test_every_generated_variant(shape):
 def test_generated_selection_covers_all_token_counts():
     for shape in tilegen.DECLARED:
         spec = TRSpec(shape.ins, shape.outs, shape.rank)
-        cores = make_cores(spec, device="cuda", dtype=torch.bfloat16, seed=1)
+        dtype = torch.bfloat16 if shape.dtype == "bf16" else torch.float16
+        cores = make_cores(spec, device="cuda", dtype=dtype, seed=1)
         run = prepare_optimized(cores, spec)
         for T in (1, 2, 3, 8, 16, 17, 64, 65, 128, 1000):
             assert run.selected(T)["kind"] == "mfma", (shape.key, T)

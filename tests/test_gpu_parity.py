@@ -96,15 +96,18 @@ def test_zero_and_scaled_inputs():
 def test_token_counts_beyond_one_launch():
     """More tokens than one launch's grid holds (65535 token tiles) split into consecutive
     launches; rows on both sides of each split are checked, with and without an epilogue."""
+    from factorized_inference import _lib
+
     spec = TRSpec(rank=8)
     cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=12)
     run = prepare_optimized(cores, spec)
     tokens = 70_000
-    assert run.selected(tokens)["tile"][0] == 1  # a one-token tile: 65535 tokens per launch
+    # a one-token tile: 65535 tokens per launch, so 70,000 tokens take two launches
+    variant = next(i for i, v in enumerate(run.variants()) if v["kind"] == "mfma" and v["tile"][0] == 1)
     x = gpu_x(spec, tokens, 3, torch.float16)
-    announce(test="beyond one launch", tokens=tokens)
-    y = run(x)
-    y32 = run.accumulate(x)
+    announce(test="beyond one launch", tokens=tokens, variant=run.variants()[variant]["name"])
+    y = run.run_variant(x, variant)
+    y32 = run.run_variant(x, variant, _lib.EPI_F32)
     torch.cuda.synchronize()
     rows = torch.tensor([0, 1, 65534, 65535, 65536, tokens - 1], device="cuda")
     check_result(y[rows], oracle_y(x[rows], cores, spec), torch.float16)
