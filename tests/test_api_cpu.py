@@ -147,6 +147,25 @@ def test_library_exports_every_declared_symbol():
     assert lib.trk_empty_call() == 0
 
 
+def test_c_program_uses_the_abi(tmp_path):
+    """A C host program compiled against include/trk.h and linked to libtrk.so: the boundary
+    as another language's binding sees it (host-side entry points, no GPU needed)."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc is not available")
+    lib_dir = _lib.LIBRARY.parent
+    exe = tmp_path / "c_abi_check"
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Werror", f"-I{ROOT / 'include'}",
+                    str(ROOT / "tests" / "c_abi_check.c"), "-o", str(exe), f"-L{lib_dir}",
+                    "-l:libtrk.so", f"-Wl,-rpath,{lib_dir}"], check=True)
+    done = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert done.returncode == 0, done.stdout + done.stderr
+    assert "all checks passed" in done.stdout
+
+
 def test_call_bindings_load_and_check_their_arguments():
     from factorized_inference import _trkcall, _trktorch
 

@@ -161,6 +161,51 @@ def test_non_contiguous_input_and_side_stream():
     check_result(y, expected, torch.float16)
 
 
+def test_one_object_on_concurrent_streams_and_threads():
+    """No state survives a call, so one prepared object serves several streams and host threads
+    at once (the reference's design B must not: tr_kernel.py:185-187). Results are bitwise
+    equal to the same calls made one at a time on the default stream."""
+    import threading
+
+    spec = TRSpec(rank=16)
+    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=14)
+    run = prepare_optimized(cores, spec)
+    xs = [gpu_x(spec, T, 60 + T, torch.float16) for T in (1, 3, 8, 32, 1, 5)]
+    expected = [run(x) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = [None] * len(xs)
+    for rep in range(3):                    # interleaved launches on two streams
+        for i, x in enumerate(xs):
+            with torch.cuda.stream(streams[i % 2]):
+                outs[i] = run(x)
+    torch.cuda.synchronize()
+    for y, e in zip(outs, expected):
+        assert torch.equal(y, e)
+    results = {}
+
+    def worker(k):                          # two host threads, each with its own stream
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.default_stream())
+        with torch.cuda.stream(stream):
+            ys = [run(x) for x in xs for _ in range(2)]
+        stream.synchronize()
+        results[k] = ys
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    for k in range(2):
+        ys = results[k]
+        for j, y in enumerate(ys):
+            assert torch.equal(y, expected[j // 2]), (k, j)
+    check_result(expected[3], oracle_y(xs[3], cores, spec), torch.float16)
+
+
 # ---- every variant the plan holds (tools/check_v3.py / check_v3t.py) ------------------------
 @pytest.mark.parametrize("shape,rank,dtype", [
     (DEFAULT, 8, torch.float16), (DEFAULT, 16, torch.float16),
