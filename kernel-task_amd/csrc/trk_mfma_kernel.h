@@ -24,6 +24,8 @@
 //   its 4 results as one 8-byte vector in exactly the layout the next stage reads.
 //   Stage 3 accumulates Y in registers over all steps; with fewer Y tiles than waves, its K
 //   range is split over waves and the partial tiles are summed through LDS at the end.
+//   Pipelined tiles (PIPE) double-buffer the last-core and x slices so that stage 3 of a
+//   step and stage 1 of the next share one barrier interval: two barriers per step, not four.
 // * 16x16x32 MFMAs (16x16x16 for a trailing K of 16), wave64, 4 or 8 waves per workgroup;
 //   the register-resident (WIDE) family runs stage 2 on 32x32x16 MFMAs.
 //
@@ -99,6 +101,9 @@ struct KCfg {
     int MF2;                 // WIDE stage-2 MFMA: 16 (16x16x32) or 32 (32x32x16, twice the
                              // matrix-core throughput of 16x16x32 on gfx950)
     int NW;                  // waves per workgroup: 4 (one per SIMD) or 8 (two per SIMD)
+    int PIPE;                // 1: the last-core and x slices are double-buffered, and stage 3
+                             // of a step shares a barrier interval with stage 1 of the next
+                             // (two barriers per step instead of four); 0: one buffer
 };
 
 template <KCfg C>
@@ -152,9 +157,10 @@ struct Geo {
     static constexpr int M2T32 = cdiv(M2, 32), N2T32 = cdiv(N2, 32);
     static constexpr int BM1 = cdiv(M1T, NW), BM2 = cdiv(W32 ? M2T32 : M2T, WM2);
     static constexpr int N2R = W32 ? N2T32 * 32 : N2P;  // Ub rows (the last tile's padding)
+    static constexpr int NBUF = C.PIPE ? 2 : 1;  // buffers of the per-step slices
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
-    static constexpr int oXs = oLs + szLs, szXs = N1P * PF;
-    static constexpr int oUb = oXs + szXs, szUb = N2R * P2;
+    static constexpr int oXs = oLs + NBUF * szLs, szXs = N1P * PF;
+    static constexpr int oUb = oXs + NBUF * szXs, szUb = N2R * P2;
     static constexpr int oVb = oUb + szUb, szVb = M3P * P3;
     static constexpr int LDS_ELEMS = oVb + szVb;
     static constexpr int LDS_BYTES = LDS_ELEMS * 2;
@@ -183,6 +189,7 @@ struct Geo {
     static_assert(LDS_BYTES <= 160 * 1024, "workgroup tile exceeds the 160 KB of LDS");
     static_assert(RED_FLOATS * 4 <= szUb * 2, "stage-3 reduction does not fit in Ub");
     static_assert(nL % IC == 0, "IC must divide the last core's input mode");
+    static_assert(C.PIPE == 0 || (C.PIPE == 1 && NSTEP > 1), "a pipelined tile needs two steps");
     static_assert(XROW || IN % 8 == 0, "scatter loader reads x rows in 8-element vectors");
 };
 
@@ -516,8 +523,8 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     // buffer never alias reads of another, so it can hoist fragment reads across stores.
     __shared__ __attribute__((aligned(16))) E Fs[G::szFs];
     __shared__ __attribute__((aligned(16))) E Ss[G::szSs];
-    __shared__ __attribute__((aligned(16))) E Ls[G::szLs];
-    __shared__ __attribute__((aligned(16))) E Xs[G::szXs];
+    __shared__ __attribute__((aligned(16))) E Ls[G::NBUF * G::szLs];
+    __shared__ __attribute__((aligned(16))) E Xs[G::NBUF * G::szXs];
     __shared__ __attribute__((aligned(16))) E Ub[G::szUb];
     __shared__ __attribute__((aligned(16))) E Vb[G::szVb];
 
@@ -564,7 +571,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             r = reinterpret_cast<const uint4 *>(x + size_t(t0) * G::IN)[v];
         return r;
     };
-    auto x_scatter_store = [&](int v, uint4 r, int iL0) {
+    auto x_scatter_store = [&](int v, uint4 r, int iL0, E *xs) {
         const int t = v / (G::IN / 8);
         if (v >= G::NXB || t0 + t >= T) return;
         const E *e = reinterpret_cast<const E *>(&r);
@@ -574,7 +581,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             const int m0 = flat / (C.i1 * C.i2), m1 = (flat / C.i2) % C.i1, m2 = flat % C.i2;
             const int iF = pick(C.F, m0, m1, m2), iS = pick(C.S, m0, m1, m2);
             const int ilp = pick(C.L, m0, m1, m2) - iL0;
-            if (ilp >= 0 && ilp < G::IC) Xs[((ilp * G::TT + t) * G::nSP + iS) * G::PF + iF] = e[q];
+            if (ilp >= 0 && ilp < G::IC) xs[((ilp * G::TT + t) * G::nSP + iS) * G::PF + iF] = e[q];
         }
     };
     RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT> cF;
@@ -590,20 +597,21 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * G::NT);
         }
     };
-    auto commit_step = [&](int iL0) {
+    auto commit_step = [&](int iL0, int buf) {  // into buffer `buf` of Ls and Xs
+        E *ls = Ls + buf * G::szLs, *xs = Xs + buf * G::szXs;
         wait_loads();
-        cL.commit(Ls);
+        cL.commit(ls);
         if constexpr (G::XROW) {
 #pragma unroll
             for (int j = 0; j < XREG; ++j) {
                 const int v = tid + j * G::NT;
                 if (G::NXV % G::NT == 0 || v < G::NXV)
-                    *reinterpret_cast<XV *>(Xs + (v / G::XCPR) * G::PF + (v % G::XCPR) * G::VX) =
+                    *reinterpret_cast<XV *>(xs + (v / G::XCPR) * G::PF + (v % G::XCPR) * G::VX) =
                         xr[j];
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < XREG; ++j) x_scatter_store(tid + j * G::NT, xb[j], iL0);
+            for (int j = 0; j < XREG; ++j) x_scatter_store(tid + j * G::NT, xb[j], iL0, xs);
             for (int j0 = XREG; j0 < XPER; j0 += XREG) {  // further batches, one latency each
 #pragma unroll
                 for (int j = 0; j < XREG; ++j)
@@ -612,7 +620,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                 wait_loads();
 #pragma unroll
                 for (int j = 0; j < XREG; ++j)
-                    if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * G::NT, xb[j], iL0);
+                    if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * G::NT, xb[j], iL0, xs);
             }
         }
     };
@@ -636,13 +644,14 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     // tokens (TT > 1) to this fill, which writes only those.
     if constexpr (!G::XROW && (G::KF > G::nF || G::nSP > G::nS || G::TT > 1)) {
         constexpr int CH = G::KF / 8;  // 16-byte chunks per row
-        for (int i = tid; i < G::N1 * CH; i += G::NT) {
-            const int n = i / CH, c = i % CH;
+        for (int i = tid; i < G::NBUF * G::N1 * CH; i += G::NT) {  // every buffer of Xs
+            const int b = i / (G::N1 * CH), n = (i / CH) % G::N1, c = i % CH;
+            E *xs = Xs + b * G::szXs;
             const bool empty_row = n % G::nSP >= G::nS || t0 + (n / G::nSP) % G::TT >= T;
             if (empty_row || 8 * c >= G::nF) {
-                *reinterpret_cast<uint4 *>(Xs + n * G::PF + 8 * c) = make_uint4(0u, 0u, 0u, 0u);
+                *reinterpret_cast<uint4 *>(xs + n * G::PF + 8 * c) = make_uint4(0u, 0u, 0u, 0u);
             } else if (G::nF % 8 != 0 && 8 * c + 8 > G::nF) {
-                for (int e = G::nF; e < 8 * c + 8; ++e) Xs[n * G::PF + e] = E(0.0f);
+                for (int e = G::nF; e < 8 * c + 8; ++e) xs[n * G::PF + e] = E(0.0f);
             }
         }
     }
@@ -651,7 +660,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         for (int i = tid; i < G::N2R * pad; i += G::NT)
             Ub[(i / pad) * G::P2 + G::nS * R + i % pad] = E(0.0f);
     }
-    commit_step(0);
+    commit_step(0, 0);
     if constexpr (!G::WIDE) {
         cF.commit(Fs);
         cS.commit(Ss);
@@ -689,27 +698,18 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     constexpr int K3STEPS = G::K3 / 32, PERK = K3STEPS / G::KS3;
     static_assert(K3STEPS % G::KS3 == 0, "stage-3 K steps must split evenly over KS3 waves");
 
-    for (int step = 0; step < G::NSTEP; ++step) {
-        const int iL0 = step * G::IC;
-        if (step > 0) {
-            __syncthreads();  // stage 3 of the previous step is done with Ls and Vb
-            commit_step(iL0);  // its loads were issued at the start of the previous step
-            __syncthreads();
-        }
-        // prefetch the next step's last-core slice and x into registers; they land while
-        // this step computes, so a step pays no memory latency of its own
-        if (step + 1 < G::NSTEP) issue_step(iL0 + G::IC);
-
+    auto put4 = [&](E *dst, f32x4 d) {
+        E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
+        *reinterpret_cast<E4 *>(dst) = h;
+    };
+    // stage 1 on the x slice in xs (a buffer of Xs)
+    auto stage1 = [&](const E *xs) {
         // stage 1: U^T = F . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]. A tile (mt, nt) stores at
         // ub_tile(mt, nt) + ub_lane: the rows (f, r1, r2) of mt*16 + 4*lgrp and the columns
         // (iL', t, iS) of nt*16 + lrow split into tile and lane parts (R and 16 are powers of
         // two and nSP is a multiple of 16, so no part carries into another).
-        auto put4 = [&](E *dst, f32x4 d) {
-            E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
-            *reinterpret_cast<E4 *>(dst) = h;
-        };
         if constexpr (G::WIDE) {
-            reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T, 1>(fa, Xs, 0, lrow, lgrp, [&](int nt, const f32x4 *d) {
+            reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T, 1>(fa, xs, 0, lrow, lgrp, [&](int nt, const f32x4 *d) {
                 if (G::nS % 16 != 0 && (nt % (G::nSP / 16)) * 16 + lrow >= G::nS) return;
 #pragma unroll
                 for (int i = 0; i < G::BM1; ++i) {
@@ -718,13 +718,13 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                 }
             });
         } else {
-            lds_gemm<O, G::M1T, G::N1T, G::KF, G::PF, G::NW>(Fs, Xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            lds_gemm<O, G::M1T, G::N1T, G::KF, G::PF, G::NW>(Fs, xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
                 if (G::nS % 16 == 0 || (nt % (G::nSP / 16)) * 16 + lrow < G::nS)
                     put4(Ub + ub_lane + ub_tile(mt, nt), d);
             });
         }
-        __syncthreads();
-
+    };
+    auto stage2 = [&]() {
         // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)], rows (s, r3) of mt*16 + 4*lgrp
         // and columns (iL', r1, t, f) of nt*16 + lrow split into tile and lane parts alike
         if constexpr (G::W32) {
@@ -759,8 +759,9 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                     put4(Vb + vb_lane + vb_tile(mt, nt), d);
             });
         }
-        __syncthreads();
-
+    };
+    // stage 3 on the last-core slice in ls (a buffer of Ls)
+    auto stage3 = [&](const E *ls) {
         // stage 3: Y[(t,f,s), l] += Vb . Ls; each wave of a group takes PERK of the K steps,
         // reading the fragments of QB steps before running their MFMAs
         constexpr int QB = PERK < 16 ? PERK : 16;
@@ -780,13 +781,56 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                         const int k = (part3 * PERK + q0 + q) * 32;
                         af[q] = *reinterpret_cast<const typename O::V8 *>(a + k + 8 * lgrp);
                         bf[q] = *reinterpret_cast<const typename O::V8 *>(
-                            Ls + ((k / R2) * G::LCP + l) * G::PL + k % R2 + 8 * lgrp);
+                            ls + ((k / R2) * G::LCP + l) * G::PL + k % R2 + 8 * lgrp);
                     }
 #pragma unroll
                     for (int q = 0; q < QB; ++q)
                         acc[j][q % G::NACC] = O::k32(af[q], bf[q], acc[j][q % G::NACC]);
                 }
             }
+        }
+    };
+
+    if constexpr (C.PIPE) {
+        // Two buffers of Ls and Xs. Step k+1's slices are committed while step k's are still
+        // being read, and stage 3 of step k runs in the same barrier interval as stage 1 of
+        // step k+1 (they touch disjoint buffers: Vb and Ls[k] against Xs[k+1] and Ub), so a
+        // step costs two barriers and each wave has two stages' MFMAs to interleave.
+        //   before the loop: Ls/Xs[0] committed; stage 1(0); barrier; stage 2(0)
+        //   step k: commit k+1 into buffer (k+1)&1; barrier; issue loads of k+2;
+        //           stage 3(k) on Ls[k&1] and stage 1(k+1) on Xs[(k+1)&1]; barrier; stage 2(k+1)
+        // Buffer (k+1)&1 was last read by stage 3(k-1) and stage 1(k-1), both before the
+        // second barrier of step k-1.
+        issue_step(G::IC);
+        stage1(Xs);
+        __syncthreads();
+        stage2();
+        for (int step = 0; step < G::NSTEP; ++step) {
+            const int next = step + 1;
+            if (next < G::NSTEP) commit_step(next * G::IC, next & 1);
+            __syncthreads();
+            if (next + 1 < G::NSTEP) issue_step((next + 1) * G::IC);
+            stage3(Ls + (step & 1) * G::szLs);
+            if (next < G::NSTEP) stage1(Xs + (next & 1) * G::szXs);
+            __syncthreads();
+            if (next < G::NSTEP) stage2();
+        }
+    } else {
+        for (int step = 0; step < G::NSTEP; ++step) {
+            const int iL0 = step * G::IC;
+            if (step > 0) {
+                __syncthreads();  // stage 3 of the previous step is done with Ls and Vb
+                commit_step(iL0, 0);  // its loads were issued at the start of the previous step
+                __syncthreads();
+            }
+            // prefetch the next step's last-core slice and x into registers; they land while
+            // this step computes, so a step pays no memory latency of its own
+            if (step + 1 < G::NSTEP) issue_step(iL0 + G::IC);
+            stage1(Xs);
+            __syncthreads();
+            stage2();
+            __syncthreads();
+            stage3(Ls);
         }
     }
 
@@ -910,9 +954,9 @@ struct Shape {
     int dt, F, S, L, i0, i1, i2, o0, o1, o2, R;
 };
 constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
-                    int WIDE = 0, int MF2 = 16, int NW = 4) {
+                    int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0) {
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
-                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW};
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE};
 }
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>},
@@ -945,13 +989,14 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
         v.t_max = e.t_max;
         v.launch = e.launch;
         if (k.WIDE)
-            std::snprintf(v.name, sizeof(v.name), "ring3_mfma_wide%d%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
-                          k.WIDE, k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "", k.F, k.S, k.L,
-                          k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
+            std::snprintf(v.name, sizeof(v.name),
+                          "ring3_mfma_wide%d%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
+                          k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "", k.PIPE ? "p" : "", k.F,
+                          k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         else
-            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
-                          k.NW == 8 ? "_w8" : "", k.F, k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC,
-                          k.KS3, k.NACC);
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+                          k.NW == 8 ? "_w8" : "", k.PIPE ? "_p" : "", k.F, k.S, k.L, k.TT, k.FC,
+                          k.SC, k.LC, k.IC, k.KS3, k.NACC);
         ++added;
     }
     return added;

@@ -27,7 +27,7 @@ from __future__ import annotations
 
 import json
 import re
-from dataclasses import asdict, dataclass, field
+from dataclasses import asdict, dataclass, field, replace
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
@@ -83,12 +83,15 @@ class Tile:
     WIDE: int = 0
     MF2: int = 16
     NW: int = 4
+    PIPE: int = 0  # double-buffered last-core and x slices, two barriers per step
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
         a = [self.TT, self.FC, self.SC, self.LC, self.IC, self.KS3, self.NACC]
-        if (self.WIDE, self.MF2, self.NW) != (0, 16, 4):
+        if (self.WIDE, self.MF2, self.NW, self.PIPE) != (0, 16, 4, 0):
             a += [self.WIDE, self.MF2, self.NW]
+        if self.PIPE:
+            a.append(self.PIPE)
         return ", ".join(map(str, a))
 
 
@@ -186,11 +189,12 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     BM1 = cdiv(M1T, NW)
     BM2 = cdiv(M2T32 if W32 else M2T, WM2)
     N2R = N2T32 * 32 if W32 else N2P
+    nbuf = 2 if t.PIPE else 1
     sz = {
         "Fs": 8 if wide else M1 * PF,
         "Ss": 8 if wide else M2P * P2,
-        "Ls": t.IC * LCP * PL,
-        "Xs": N1 * PF,
+        "Ls": nbuf * t.IC * LCP * PL,
+        "Xs": nbuf * N1 * PF,
         "Ub": N2R * P2,
         "Vb": M3P * P3,
     }
@@ -219,6 +223,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (t.FC <= c.oF and t.SC <= c.oS and t.LC <= c.oL and t.IC <= c.nL and t.TT >= 1,
          "tile too large"),
         (c.nL % t.IC == 0, "IC must divide the last core's input mode"),
+        (t.PIPE in (0, 1) and (t.PIPE == 0 or c.nL // t.IC > 1), "a pipelined tile needs two steps"),
         (c.xrow or c.IN % 8 == 0, "scatter loader reads x rows in 8-element vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= sz["Ub"] * 2, "stage-3 reduction does not fit in Ub"),
@@ -301,15 +306,43 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
         for tt in (2, 4):
             add(f"mid_half_t{tt}", lambda ic, tt=tt: Tile(tt, 1, half, LC, ic, 1, 2), ics)
             add(f"mid_all_t{tt}", lambda ic, tt=tt: Tile(tt, 1, c.oS, LC, ic, 1, 2), ics)
+        # a quarter or an eighth of the second core's outputs per workgroup, stage 3's K
+        # split over two waves when the K steps allow it
+        for part in (4, 8):
+            sc = cdiv(c.oS, part)
+            if 2 < sc < half:
+                for ks3 in (2, 1):
+                    before = len(out)
+                    add(f"mid_1of{part}_k{ks3}", lambda ic, sc=sc, ks3=ks3: Tile(
+                        1, 1, sc, LC, ic, ks3, 2), ics)
+                    if len(out) > before:
+                        break
         for wide, nw in ((4, 4), (8, 8)):
-            base = out.get(f"wide{wide}x32" + ("w8" if nw == 8 else ""))
+            fam = f"wide{wide}x32" + ("w8" if nw == 8 else "")
+            base = out.get(fam)
             if base is None:
                 continue
-            for tt, ks3, nacc in ((8, 2, 1), (4, 1, 2), (8, 1, 2)):
-                add(f"wide{wide}x32{'w8' if nw == 8 else ''}_t{tt}k{ks3}n{nacc}",
+            for tt, ks3, nacc in ((8, 2, 1), (4, 1, 2), (8, 1, 2), (2, 1, 4), (2, 1, 2)):
+                add(f"{fam}_t{tt}k{ks3}n{nacc}",
                     lambda ic, tt=tt, ks3=ks3, nacc=nacc, base=base: Tile(
                         tt, 1, base.SC, LC, ic, ks3, nacc, wide, 32, nw),
                     [base.IC] + [d for d in ics if d < base.IC])
+            # more last-core inputs per step (fewer steps and barriers), over the register
+            # budget if need be: a few spilled registers may still win
+            for mult in (2, 4):
+                ic = base.IC * mult
+                if ic > c.nL or c.nL % ic:
+                    continue
+                for tt, ks3, nacc in ((4, 2, 1), (4, 1, 2)):
+                    t = Tile(tt, 1, base.SC, LC, ic, ks3, nacc, wide, 32, nw)
+                    if not geometry(shape, order, t)["reject"] and t not in out.values():
+                        out[f"{fam}_t{tt}k{ks3}n{nacc}_ic{ic}"] = t
+        # the pipelined main loop for every multi-step tile found so far that still fits
+        for name, t in list(out.items()):
+            if cdiv(c.nL, t.IC) > 1:
+                p = replace(t, PIPE=1)
+                if not geometry(shape, order, p)["reject"] and p not in out.values():
+                    out[name + "_p"] = p
     if not any(n.startswith("wide") for n in out):
         # no register-resident tile within the budget (a long stage-2 K): offer the smallest
         # over-budget one, which may spill a few registers; the autotuner decides
@@ -320,7 +353,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
     return out
 
 
-_VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?|(_w8))?<(\d)(\d)(\d),"
+_VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p)?|(_w8)?(_p)?)<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -330,10 +363,11 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     if not m:
         raise ValueError(f"not an MFMA variant name: {name!r}")
     wide = int(m.group(1) or 0)
-    order = tuple(int(m.group(i)) for i in (5, 6, 7))
-    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(8, 15))
+    order = tuple(int(m.group(i)) for i in (7, 8, 9))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(10, 17))
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
-                       8 if (m.group(3) or m.group(4)) else 4)
+                       8 if (m.group(3) or m.group(5)) else 4,
+                       1 if (m.group(4) or m.group(6)) else 0)
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
@@ -381,6 +415,12 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
     order = choose_order(shape)
     cands = candidates(shape, order, extended)
     ranges = rule_ranges(list(cands))
+    if all_candidates and tuned.get(shape.key, {}).get("order") == list(order):
+        # the previous winners stay candidates, so a new search never loses a tile it had
+        for r in tuned[shape.key]["ranges"]:
+            t = Tile(**r["tile"])
+            if t not in cands.values():
+                cands[r["name"]] = t
     return order, [(n, t, *ranges.get(n, (0, 0))) for n, t in cands.items()]
 
 

@@ -7,7 +7,8 @@
 - Every declared shape gets MFMA variants whose default token ranges cover every token
   count, in the chain order the generator chose.
 - Planted mistakes in a tile (a rank that is not a power of two, FC*TT not dividing 16, IC
-  not dividing the last core's input mode, LDS over budget) are rejected.
+  not dividing the last core's input mode, LDS over budget, a pipelined tile of one step, a
+  pipelined tile whose doubled slices no longer fit) are rejected.
 """
 from __future__ import annotations
 
@@ -36,6 +37,11 @@ def test_variant_names_parse_back_to_their_tiles():
     assert parse("ring3_mfma_wide8x32w8<012,4,1,28,32,4,1,2>") == (
         (0, 1, 2), tilegen.Tile(4, 1, 28, 32, 4, 1, 2, 8, 32, 8))
     assert parse("ring3_mfma_wide2<210,4,1,8,16,1,2,1>")[1].MF2 == 16
+    assert parse("ring3_mfma_wide8x32w8p<210,8,1,10,12,1,1,2>")[1] == tilegen.Tile(
+        8, 1, 10, 12, 1, 1, 2, 8, 32, 8, 1)
+    assert parse("ring3_mfma_w8_p<210,1,1,1,12,4,8,1>")[1] == tilegen.Tile(
+        1, 1, 1, 12, 4, 8, 1, 0, 16, 8, 1)
+    assert parse("ring3_mfma_p<210,1,1,10,12,2,1,2>")[1].PIPE == 1
     with pytest.raises(ValueError):
         parse("ring3_generic<012,rc=8>")
 
@@ -97,6 +103,8 @@ def test_order_choice_prefers_least_padded_work():
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 3, 1, 1), "IC must divide"),
     (HAND[1], tilegen.Tile(1, 1, 10, 12, 8, 1, 1), "LDS"),
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 3, 1), "KS3"),
+    (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, PIPE=1), "two steps"),
+    (HAND[1], tilegen.Tile(1, 1, 5, 12, 4, 1, 2, PIPE=1), "LDS"),  # fits with one buffer
 ])
 def test_planted_tile_mistakes_are_rejected(shape, tile, why):
     assert why in tilegen.geometry(shape, (2, 1, 0), tile)["reject"]
