@@ -157,6 +157,14 @@ struct Geo {
     static constexpr int M2T32 = cdiv(M2, 32), N2T32 = cdiv(N2, 32);
     static constexpr int BM1 = cdiv(M1T, NW), BM2 = cdiv(W32 ? M2T32 : M2T, WM2);
     static constexpr int N2R = W32 ? N2T32 * 32 : N2P;  // Ub rows (the last tile's padding)
+    // W32 with one row tile per wave and fewer row tiles than waves (8): waves 0-3 take a row
+    // tile each and waves 4-7 split the TAILR remaining row tiles' columns TAILJ ways. Waves
+    // w and w+4 share a SIMD, so every SIMD gets nearly equal stage-2 work (for 5 row tiles:
+    // 5 tile columns' worth on each SIMD instead of 8 on one).
+    static constexpr int TAILR = M2T32 - NW / 2;
+    static constexpr bool TAIL = W32 && WN2 == 1 && BM2 == 1 && NW == 8 && TAILR > 0 &&
+                                 M2T32 < NW && (NW / 2) % TAILR == 0;
+    static constexpr int TAILJ = TAIL ? (NW / 2) / TAILR : 1;
     static constexpr int NBUF = C.PIPE ? 2 : 1;  // buffers of the per-step slices
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
     static constexpr int oXs = oLs + NBUF * szLs, szXs = N1P * PF;
@@ -625,15 +633,19 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         }
     };
 
+    // stage-2 row group and column phase of this wave (WIDE)
+    constexpr int HW = G::NW / 2;
+    const int wm2 = G::TAIL ? (wave < HW ? wave : HW + (wave - HW) / G::TAILJ) : wave % G::WM2;
+    const int wn2 = G::TAIL ? (wave < HW ? 0 : (wave - HW) % G::TAILJ) : wave / G::WM2;
     // the first- and second-core slices stay resident for the whole call
     RegA<O, G::BM1, G::KF> fa;
     std::conditional_t<G::W32, RegA32<O, G::BM2, G::K2>, RegA<O, G::BM2, G::K2>> sa;
     if constexpr (G::WIDE) {
         fa.load(Fk + size_t(f0) * R2 * G::KF, wave * G::BM1 * 16, FCv * R2, lrow, lgrp);
         if constexpr (G::W32)
-            sa.load(Sk + size_t(s0) * R * G::K2, (wave % G::WM2) * G::BM2 * 32, SCv * R, lane);
+            sa.load(Sk + size_t(s0) * R * G::K2, wm2 * G::BM2 * 32, SCv * R, lane);
         else
-            sa.load(Sk + size_t(s0) * R * G::K2, (wave % G::WM2) * G::BM2 * 16, SCv * R, lrow, lgrp);
+            sa.load(Sk + size_t(s0) * R * G::K2, wm2 * G::BM2 * 16, SCv * R, lrow, lgrp);
     } else {
         cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
         cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
@@ -709,6 +721,8 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         // (iL', t, iS) of nt*16 + lrow split into tile and lane parts (R and 16 are powers of
         // two and nSP is a multiple of 16, so no part carries into another).
         if constexpr (G::WIDE) {
+            // a wave whose row tiles all lie past the last one has no stage-1 work
+            if (G::M1T % G::NW == 0 || wave * G::BM1 < G::M1T)
             reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T, 1>(fa, xs, 0, lrow, lgrp, [&](int nt, const f32x4 *d) {
                 if (G::nS % 16 != 0 && (nt % (G::nSP / 16)) * 16 + lrow >= G::nS) return;
 #pragma unroll
@@ -728,26 +742,33 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)], rows (s, r3) of mt*16 + 4*lgrp
         // and columns (iL', r1, t, f) of nt*16 + lrow split into tile and lane parts alike
         if constexpr (G::W32) {
-            const int wm = wave % G::WM2, wn = wave / G::WM2;
-            reg_gemm32<O, G::BM2, G::K2, G::P2, G::N2T32, G::WN2>(sa, Ub, wn, lane, [&](int nt, const f32x16 *d) {
+            auto st = [&](int nt, const f32x16 *d) {
                 if (G::N2 % 32 != 0 && nt * 32 + (lane & 31) >= G::N2) return;
 #pragma unroll
                 for (int i = 0; i < G::BM2; ++i) {
-                    const int mt = wm * G::BM2 + i;
+                    const int mt = wm2 * G::BM2 + i;
 #pragma unroll
                     for (int g = 0; g < 4; ++g)
                         if (G::M2 % (32 * G::WM2) == 0 || mt * 32 + 8 * g + 4 * (lane >> 5) < G::M2)
                             put4(Vb + vb_lane32 + vb_tile32(mt, nt) + vb_row(8 * g),
                                  f32x4{d[i][4 * g], d[i][4 * g + 1], d[i][4 * g + 2], d[i][4 * g + 3]});
                 }
-            });
+            };
+            if constexpr (G::TAIL) {
+                if (wave < HW)
+                    reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, 1>(sa, Ub, 0, lane, st);
+                else
+                    reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, G::TAILJ>(sa, Ub, wn2, lane, st);
+            } else if (G::M2T32 % G::WM2 == 0 || wm2 * G::BM2 < G::M2T32) {  // else no rows
+                reg_gemm32<O, G::BM2, G::K2, G::P2, G::N2T32, G::WN2>(sa, Ub, wn2, lane, st);
+            }
         } else if constexpr (G::WIDE) {
-            const int wm = wave % G::WM2, wn = wave / G::WM2;
-            reg_gemm<O, G::BM2, G::K2, G::P2, G::N2T, G::WN2>(sa, Ub, wn, lrow, lgrp, [&](int nt, const f32x4 *d) {
+            if (G::M2T % G::WM2 == 0 || wm2 * G::BM2 < G::M2T)  // else this wave has no rows
+            reg_gemm<O, G::BM2, G::K2, G::P2, G::N2T, G::WN2>(sa, Ub, wn2, lrow, lgrp, [&](int nt, const f32x4 *d) {
                 if (G::N2 % 16 != 0 && nt * 16 + lrow >= G::N2) return;
 #pragma unroll
                 for (int i = 0; i < G::BM2; ++i) {
-                    const int mt = wm * G::BM2 + i;
+                    const int mt = wm2 * G::BM2 + i;
                     if (G::M2 % (16 * G::WM2) == 0 || mt * 16 + 4 * lgrp < G::M2)
                         put4(Vb + vb_lane + vb_tile(mt, nt), d[i]);
                 }
