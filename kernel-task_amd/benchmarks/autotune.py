@@ -16,7 +16,8 @@ small token counts). Every variant's
 output is checked against the shape's default variant before it may win (bitwise equality
 is not expected across tiles: the stage-3 summation order differs).
 
-Token counts measured: 1, 2, 4, 8, 16, 32, 64, 128, 256. The winner at T serves the range
+Candidates span every chain order the generator searches (tilegen.search_orders); each
+range records its winner's order. Token counts measured: 1, 2, 4, 8, 16, 32, 64, 128, 256. The winner at T serves the range
 (previous measured T, T]; 256's winner serves everything above.
 """
 from __future__ import annotations
@@ -75,11 +76,11 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
     run = prepare_optimized(cores, spec)
     variants = [(i, v) for i, v in enumerate(run.variants()) if v["kind"] == "mfma"]
     names, tiles = {}, {}
-    cands = tilegen.candidates(shape, extended=True)
+    cands = tilegen.search_candidates(shape, extended=True)
     for i, v in variants:
-        order, tile = tilegen.parse_variant_name(v["name"])
-        names[i] = next((n for n, t in cands.items() if t == tile), v["name"])
-        tiles[names[i]] = tile
+        key = tilegen.parse_variant_name(v["name"])
+        names[i] = next((n for n, c in cands.items() if c == key), v["name"])
+        tiles[names[i]] = key
     measured: dict[int, dict[str, float]] = {}
     t_end = time.perf_counter() + budget_s
     for T in GRID:
@@ -128,7 +129,8 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
         lo = T + 1
     order = tilegen.choose_order(shape)
     for r in ranges:
-        r["tile"] = asdict(tiles[r["name"]])
+        r["order"] = list(tiles[r["name"]][0])
+        r["tile"] = asdict(tiles[r["name"]][1])
     return {"order": list(order), "device": torch.cuda.get_device_name(0),
             "measured_us": {str(T): row for T, row in measured.items()}, "ranges": ranges}
 

@@ -26,7 +26,8 @@
 //   range is split over waves and the partial tiles are summed through LDS at the end.
 //   Pipelined tiles (PIPE) double-buffer the last-core and x slices so that stage 3 of a
 //   step and stage 1 of the next share one barrier interval: two barriers per step, not four.
-// * 16x16x32 MFMAs (16x16x16 for a trailing K of 16), wave64, 4 or 8 waves per workgroup;
+// * 16x16x32 MFMAs (16x16x16 for a K of 16 alone; a trailing 16 after 32-wide steps is one
+//   more 16x16x32 MFMA with a zero upper half), wave64, 4 or 8 waves per workgroup;
 //   the register-resident (WIDE) family runs stage 2 on 32x32x16 MFMAs.
 //
 // Variants are compiled for the declared shapes and their tuned token ranges; plans for
@@ -311,7 +312,28 @@ __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename 
 #pragma unroll
                 for (int q = 0; q < BN; ++q) d[i][q] = O::k32(af[i], bf[q], d[i][q]);
         }
-        if constexpr (K16) {
+        if constexpr (K16 && K32 > 0) {
+            // trailing 16 of K after 32-wide steps: one more 16x16x32 MFMA whose upper K half
+            // (lanes 32-63) is zero, so the accumulation chain never mixes MFMA shapes (a
+            // 16x16x16 MFMA reading the accumulator of a 16x16x32 one back to back has given
+            // wrong sums on gfx950)
+            V8 af[BM], bf[BN];
+            const int kt = K - 16 + 8 * (lgrp & 1);  // stays inside the row for every lane
+#pragma unroll
+            for (int i = 0; i < BM; ++i)
+                af[i] = (lgrp < 2 && (MT % BM == 0 || m0 + i < MT))
+                            ? *reinterpret_cast<const V8 *>(a + i * 16 * P + kt)
+                            : V8{};
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                bf[q] = (lgrp < 2 && (NT % BN == 0 || n0 + q < NT))
+                            ? *reinterpret_cast<const V8 *>(b + q * 16 * P + kt)
+                            : V8{};
+#pragma unroll
+            for (int i = 0; i < BM; ++i)
+#pragma unroll
+                for (int q = 0; q < BN; ++q) d[i][q] = O::k32(af[i], bf[q], d[i][q]);
+        } else if constexpr (K16) {  // K of 16 alone: one 16x16x16 MFMA per tile
             V4 af[BM], bf[BN];
 #pragma unroll
             for (int i = 0; i < BM; ++i)
@@ -344,7 +366,8 @@ template <class O, int BMW, int K>
 struct RegA {
     static constexpr int K32 = K / 32, K16 = (K % 32) / 16;
     typename O::V8 a8[BMW][K32 > 0 ? K32 : 1];
-    typename O::V4 a4[BMW];
+    typename O::V4 a4[BMW];  // a K of 16 alone (16x16x16 fragments)
+    typename O::V8 t8[BMW];  // a trailing 16 after 32-wide steps, upper K half zero
     __device__ __forceinline__ void load(const typename O::E *__restrict__ src, int row0, int rows,
                                          int lrow, int lgrp) {
 #pragma unroll
@@ -355,7 +378,11 @@ struct RegA {
             for (int k = 0; k < K32; ++k)
                 a8[i][k] = row < rows ? *reinterpret_cast<const typename O::V8 *>(p + 32 * k + 8 * lgrp)
                                       : typename O::V8{};
-            if constexpr (K16)
+            if constexpr (K16 && K32 > 0)
+                t8[i] = row < rows && lgrp < 2
+                            ? *reinterpret_cast<const typename O::V8 *>(p + K - 16 + 8 * (lgrp & 1))
+                            : typename O::V8{};
+            else if constexpr (K16)
                 a4[i] = row < rows ? *reinterpret_cast<const typename O::V4 *>(p + K - 16 + 4 * lgrp)
                                    : typename O::V4{};
         }
@@ -413,7 +440,21 @@ __device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typenam
 #pragma unroll
             for (int q = 0; q < BN; ++q) cur[q] = nxt[q];
         }
-        if constexpr (K16) {
+        if constexpr (K16 && K32 > 0) {
+            // trailing 16 of K: a 16x16x32 MFMA with the upper K half zero, so that the
+            // accumulation chain keeps one MFMA shape (as in lds_gemm)
+            V8 bf[BN];
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                bf[q] = have(q) && lgrp < 2 ? *reinterpret_cast<const V8 *>(
+                                                  b + q * WN * 16 * P + K - 16 + 8 * (lgrp & 1))
+                                            : V8{};
+#pragma unroll
+            for (int q = 0; q < BN; ++q)
+                if (have(q))
+#pragma unroll
+                    for (int i = 0; i < BMW; ++i) d[q][i] = O::k32(A.t8[i], bf[q], d[q][i]);
+        } else if constexpr (K16) {
             V4 bf[BN];
 #pragma unroll
             for (int q = 0; q < BN; ++q)

@@ -155,6 +155,27 @@ def choose_order(shape: ShapeDecl) -> tuple:
     return min(ORDERS, key=lambda o: padded_work(shape, o))
 
 
+ALT_ORDER_SLACK = 1.15  # extended search: further orders within 15 % of the least padded work
+
+
+def search_orders(shape: ShapeDecl, extended: bool = False) -> list[tuple]:
+    """Chain orders whose tiles are candidates: the shape's order, and with extended=True
+    every other order within ALT_ORDER_SLACK of the least padded work (a smaller stage-2 K
+    or a better-balanced stage-2 row count can outweigh a few percent more work)."""
+    first = choose_order(shape)
+    if not extended:
+        return [first]
+    least = min(padded_work(shape, o)[0] for o in ORDERS)
+    rest = sorted((o for o in ORDERS if o != first and
+                   padded_work(shape, o)[0] <= ALT_ORDER_SLACK * least),
+                  key=lambda o: padded_work(shape, o)[0])
+    return [first] + rest
+
+
+def order_tag(order: tuple) -> str:
+    return "".join(map(str, order))
+
+
 def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     """The kernel's compile-time geometry (struct Geo) for one tile, with the reason the
     kernel would reject it ("" when it compiles). Mirrors the static_asserts of Geo."""
@@ -397,31 +418,50 @@ def load_tuned() -> dict:
     return json.loads(TUNED.read_text()) if TUNED.exists() else {}
 
 
+def search_candidates(shape: ShapeDecl, extended: bool = False) -> dict[str, tuple[tuple, Tile]]:
+    """name -> (order, tile) over every searched order; tiles of an order other than the
+    shape's own carry the suffix @FSL in their names."""
+    first = choose_order(shape)
+    out = {}
+    for order in search_orders(shape, extended):
+        tag = "" if order == first else "@" + order_tag(order)
+        for name, t in candidates(shape, order, extended).items():
+            out[name + tag] = (order, t)
+    return out
+
+
 def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = False,
-          extended: bool = False) -> tuple[tuple, list[tuple[str, Tile, int, int]]]:
-    """(order, [(name, tile, t_min, t_max)]) for one shape: the tuned winners when the shape
+          extended: bool = False) -> list[tuple[str, tuple, Tile, int, int]]:
+    """[(name, order, tile, t_min, t_max)] for one shape: the tuned winners when the shape
     has measurements, else every candidate with the rule's ranges (0, 0: index only).
     all_candidates=True ignores the measurements (the autotuner's input)."""
     tuned = load_tuned() if tuned is None else tuned
     entry = None if all_candidates else tuned.get(shape.key)
     if entry:
-        order = tuple(entry["order"])
-        rows = [(r["name"], Tile(**r["tile"]), r["t_min"], r["t_max"]) for r in entry["ranges"]]
-        for name, t, _, _ in rows:
+        rows = [(r["name"], tuple(r.get("order", entry["order"])), Tile(**r["tile"]),
+                 r["t_min"], r["t_max"]) for r in entry["ranges"]]
+        for name, order, t, _, _ in rows:
             why = geometry(shape, order, t)["reject"]
             if why:
                 raise ValueError(f"{shape.key}: tuned tile {name} is rejected: {why}")
-        return order, rows
-    order = choose_order(shape)
-    cands = candidates(shape, order, extended)
-    ranges = rule_ranges(list(cands))
-    if all_candidates and tuned.get(shape.key, {}).get("order") == list(order):
+        return rows
+    first = choose_order(shape)
+    cands = search_candidates(shape, extended)
+    ranges = rule_ranges([n for n, (o, _) in cands.items() if o == first])
+    if all_candidates and shape.key in tuned:
         # the previous winners stay candidates, so a new search never loses a tile it had
-        for r in tuned[shape.key]["ranges"]:
-            t = Tile(**r["tile"])
-            if t not in cands.values():
-                cands[r["name"]] = t
-    return order, [(n, t, *ranges.get(n, (0, 0))) for n, t in cands.items()]
+        entry = tuned[shape.key]
+        for r in entry["ranges"]:
+            order = tuple(r.get("order", entry["order"]))
+            if order not in ORDERS:
+                continue
+            key = (order, Tile(**r["tile"]))
+            if key not in cands.values():
+                name = r["name"]
+                if order != first and "@" not in name:
+                    name += "@" + order_tag(order)
+                cands[name] = key
+    return [(n, o, t, *ranges.get(n, (0, 0))) for n, (o, t) in cands.items()]
 
 
 def _fn_name(shape: ShapeDecl) -> str:
@@ -431,7 +471,8 @@ def _fn_name(shape: ShapeDecl) -> str:
 def emit(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = False,
          extended: bool = False) -> str:
     tuned = load_tuned() if tuned is None else tuned
-    order, rows = table(shape, tuned, all_candidates, extended)
+    rows = table(shape, tuned, all_candidates, extended)
+    orders = sorted({r[1] for r in rows}, key=lambda od: (od != choose_order(shape), od))
     i, o = shape.ins, shape.outs
     tuned_note = ("token ranges measured by kernel-task_amd/benchmarks/autotune.py"
                   if tuned.get(shape.key) and not all_candidates
@@ -439,20 +480,22 @@ def emit(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fal
     lines = [
         "// Generated by kernel-task_amd/factorized_inference/tilegen.py; do not edit.",
         f"// {shape.name}: ({i[0]},{i[1]},{i[2]}) -> ({o[0]},{o[1]},{o[2]}), rank "
-        f"{shape.rank}, {shape.dtype}, chain order ({order[0]},{order[1]},{order[2]}); "
-        f"{tuned_note}.",
+        f"{shape.rank}, {shape.dtype}, chain order"
+        f"{'s' if len(orders) > 1 else ''} "
+        + ", ".join(f"({od[0]},{od[1]},{od[2]})" for od in orders) + f"; {tuned_note}.",
         '#include "trk_mfma_kernel.h"',
         "",
         "namespace trk {",
         "namespace {",
         "",
-        f"constexpr Shape kShape{{{DTYPES[shape.dtype]}, {order[0]}, {order[1]}, {order[2]}, "
-        f"{i[0]}, {i[1]}, {i[2]}, {o[0]}, {o[1]}, {o[2]}, {shape.rank}}};",
-        "",
-        "const Entry kEntries[] = {",
     ]
-    for name, t, lo, hi in rows:
-        lines.append(f"    TRK_ENTRY(tile(kShape, {t.args()}), {lo}, {hi})  // {name}")
+    for od in orders:
+        lines.append(f"constexpr Shape kShape{order_tag(od)}{{{DTYPES[shape.dtype]}, {od[0]}, "
+                     f"{od[1]}, {od[2]}, {i[0]}, {i[1]}, {i[2]}, {o[0]}, {o[1]}, {o[2]}, "
+                     f"{shape.rank}}};")
+    lines += ["", "const Entry kEntries[] = {"]
+    for name, od, t, lo, hi in rows:
+        lines.append(f"    TRK_ENTRY(tile(kShape{order_tag(od)}, {t.args()}), {lo}, {hi})  // {name}")
     lines += [
         "};",
         "",
@@ -514,13 +557,13 @@ def describe(shapes: list[ShapeDecl] = DECLARED) -> list[dict]:
     """Per shape: order, work and the tiles with their geometry (for reports and tests)."""
     out = []
     for s in shapes:
-        order, rows = table(s)
+        order = choose_order(s)
         padded, unpadded = padded_work(s, order)
         out.append({"shape": s.key, "name": s.name, "order": order,
                     "padded_mac_per_token": padded, "mac_per_token": unpadded,
-                    "tiles": [{"name": n, "tile": asdict(t), "t_min": lo, "t_max": hi,
-                               **{k: v for k, v in geometry(s, order, t).items()}}
-                              for n, t, lo, hi in rows]})
+                    "tiles": [{"name": n, "order": od, "tile": asdict(t), "t_min": lo,
+                               "t_max": hi, **geometry(s, od, t)}
+                              for n, od, t, lo, hi in table(s)]})
     return out
 
 

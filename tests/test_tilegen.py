@@ -71,15 +71,45 @@ def test_generated_sources_are_current(tmp_path):
 
 @pytest.mark.parametrize("shape", tilegen.DECLARED, ids=lambda s: s.key)
 def test_declared_shapes_are_covered(shape):
-    order, rows = tilegen.table(shape)
+    rows = tilegen.table(shape)
     plan = _lib.Plan(shape.ins, shape.outs, shape.rank, DT[shape.dtype])
     for T in (1, 2, 3, 7, 8, 16, 17, 33, 64, 65, 128, 256, 4096):
         info = plan.describe(-1, T)
         assert info["kind"] == "mfma", (shape.key, T)
+        # the selected tile is the table's tile for T, in that row's chain order
+        covering = [r for r in rows if r[3] <= T <= r[4]]
+        assert len(covering) == 1, (shape.key, T)
+        name, order, tile, _, _ = covering[0]
         assert tuple(info["order"]) == order
-    for _, tile, lo, hi in rows:
+        assert tilegen.parse_variant_name(info["name"]) == (order, tile), (name, info["name"])
+    for _, order, tile, lo, hi in rows:
         assert not tilegen.geometry(shape, order, tile)["reject"]
         assert (lo, hi) == (0, 0) or 1 <= lo <= hi
+
+
+def test_every_table_row_is_registered():
+    # a plan holds a bounded number of variants: none of a shape's tiles may be dropped
+    for shape in tilegen.DECLARED:
+        plan = _lib.Plan(shape.ins, shape.outs, shape.rank, DT[shape.dtype])
+        names = [v["name"] for v in plan.variants(1) if v["kind"] == "mfma"]
+        assert len(names) == len(tilegen.table(shape)), shape.key
+        key = lambda ot: (ot[0], tuple(vars(ot[1]).values()))  # noqa: E731
+        assert sorted(map(tilegen.parse_variant_name, names), key=key) == sorted(
+            ((order, tile) for _, order, tile, _, _ in tilegen.table(shape)), key=key)
+
+
+def test_search_orders():
+    for shape in tilegen.DECLARED:
+        orders = tilegen.search_orders(shape, extended=True)
+        assert orders[0] == tilegen.choose_order(shape) == tilegen.search_orders(shape)[0]
+        assert len(set(orders)) == len(orders)
+        least = min(tilegen.padded_work(shape, o)[0] for o in tilegen.ORDERS)
+        for o in orders[1:]:
+            assert tilegen.padded_work(shape, o)[0] <= tilegen.ALT_ORDER_SLACK * least
+    # candidates of another order carry its tag and parse back to that order
+    cands = tilegen.search_candidates(HAND[3], extended=True)
+    tagged = [n for n in cands if "@" in n]
+    assert tagged and all(cands[n][0] == tuple(int(c) for c in n.split("@")[1]) for n in tagged)
 
 
 def test_order_choice_prefers_least_padded_work():
