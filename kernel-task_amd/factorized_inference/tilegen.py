@@ -324,6 +324,12 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
     if extended:
         add("t1_s1_icall", lambda ic: Tile(1, 1, 1, LC, ic, 4, 1), ics)
         add("t1_s2_icall", lambda ic: Tile(1, 1, min(2, c.oS), LC, ic, 4, 1), ics)
+        # stage 3 on fewer waves with independent accumulator chains: no cross-wave
+        # reduction (a barrier and an LDS round trip) at the price of a longer K loop
+        for sc in (1, 2):
+            for ks3, nacc in ((1, 4), (2, 2)):
+                add(f"t1_s{sc}_k{ks3}n{nacc}", lambda ic, sc=sc, ks3=ks3, nacc=nacc: Tile(
+                    1, 1, min(sc, c.oS), LC, ic, ks3, nacc), small_ics)
         for tt in (2, 4):
             add(f"mid_half_t{tt}", lambda ic, tt=tt: Tile(tt, 1, half, LC, ic, 1, 2), ics)
             add(f"mid_all_t{tt}", lambda ic, tt=tt: Tile(tt, 1, c.oS, LC, ic, 1, 2), ics)
