@@ -104,7 +104,9 @@ struct KCfg {
     int NW;                  // waves per workgroup: 4 (one per SIMD) or 8 (two per SIMD)
     int PIPE;                // 1: the last-core and x slices are double-buffered, and stage 3
                              // of a step shares a barrier interval with stage 1 of the next
-                             // (two barriers per step instead of four); 0: one buffer
+                             // (two barriers per step instead of four); 2: the stage results
+                             // (Ub, Vb) are double-buffered too, and stages 1, 2 and 3 of three
+                             // consecutive steps share one barrier interval; 0: one buffer
 };
 
 template <KCfg C>
@@ -167,11 +169,12 @@ struct Geo {
                                  M2T32 < NW && (NW / 2) % TAILR == 0;
     static constexpr int TAILJ = TAIL ? (NW / 2) / TAILR : 1;
     static constexpr int NBUF = C.PIPE ? 2 : 1;  // buffers of the per-step slices
+    static constexpr int NBUF2 = C.PIPE == 2 ? 2 : 1;  // buffers of the stage results
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
     static constexpr int oXs = oLs + NBUF * szLs, szXs = N1P * PF;
     static constexpr int oUb = oXs + NBUF * szXs, szUb = N2R * P2;
-    static constexpr int oVb = oUb + szUb, szVb = M3P * P3;
-    static constexpr int LDS_ELEMS = oVb + szVb;
+    static constexpr int oVb = oUb + NBUF2 * szUb, szVb = M3P * P3;
+    static constexpr int LDS_ELEMS = oVb + NBUF2 * szVb;
     static constexpr int LDS_BYTES = LDS_ELEMS * 2;
     static constexpr int RED_FLOATS = (KS3 - 1) * G3 * NYW * 256;
     // x loader. Contiguous iF: VX-element vectors straight into Xs rows. Otherwise: 8-element
@@ -198,7 +201,8 @@ struct Geo {
     static_assert(LDS_BYTES <= 160 * 1024, "workgroup tile exceeds the 160 KB of LDS");
     static_assert(RED_FLOATS * 4 <= szUb * 2, "stage-3 reduction does not fit in Ub");
     static_assert(nL % IC == 0, "IC must divide the last core's input mode");
-    static_assert(C.PIPE == 0 || (C.PIPE == 1 && NSTEP > 1), "a pipelined tile needs two steps");
+    static_assert(C.PIPE >= 0 && C.PIPE <= 2 && (C.PIPE == 0 || NSTEP > 1),
+                  "a pipelined tile needs two steps");
     static_assert(XROW || IN % 8 == 0, "scatter loader reads x rows in 8-element vectors");
 };
 
@@ -574,8 +578,8 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     __shared__ __attribute__((aligned(16))) E Ss[G::szSs];
     __shared__ __attribute__((aligned(16))) E Ls[G::NBUF * G::szLs];
     __shared__ __attribute__((aligned(16))) E Xs[G::NBUF * G::szXs];
-    __shared__ __attribute__((aligned(16))) E Ub[G::szUb];
-    __shared__ __attribute__((aligned(16))) E Vb[G::szVb];
+    __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
+    __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -636,8 +640,10 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT> cF;
     RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8, G::NT> cS;
     RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, G::NT> cL;
-    auto issue_step = [&](int iL0) {
+    auto issue_l = [&](int iL0) {  // the last-core slice of the step at input digit iL0
         cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
+    };
+    auto issue_x = [&](int iL0) {  // x for the step at input digit iL0
         if constexpr (G::XROW) {
 #pragma unroll
             for (int j = 0; j < XREG; ++j) xr[j] = x_row_load(tid + j * G::NT, iL0);
@@ -646,10 +652,17 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * G::NT);
         }
     };
-    auto commit_step = [&](int iL0, int buf) {  // into buffer `buf` of Ls and Xs
-        E *ls = Ls + buf * G::szLs, *xs = Xs + buf * G::szXs;
+    auto issue_step = [&](int iL0) {
+        issue_l(iL0);
+        issue_x(iL0);
+    };
+    auto commit_l = [&](int buf) {  // into buffer `buf` of Ls
         wait_loads();
-        cL.commit(ls);
+        cL.commit(Ls + buf * G::szLs);
+    };
+    auto commit_x = [&](int iL0, int buf) {  // into buffer `buf` of Xs
+        E *xs = Xs + buf * G::szXs;
+        wait_loads();
         if constexpr (G::XROW) {
 #pragma unroll
             for (int j = 0; j < XREG; ++j) {
@@ -672,6 +685,10 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                     if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * G::NT, xb[j], iL0, xs);
             }
         }
+    };
+    auto commit_step = [&](int iL0, int buf) {  // into buffer `buf` of Ls and Xs
+        commit_l(buf);
+        commit_x(iL0, buf);
     };
 
     // stage-2 row group and column phase of this wave (WIDE)
@@ -710,7 +727,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     }
     if constexpr (G::K2 > G::nS * R) {
         constexpr int pad = G::K2 - G::nS * R;
-        for (int i = tid; i < G::N2R * pad; i += G::NT)
+        for (int i = tid; i < G::NBUF2 * G::N2R * pad; i += G::NT)  // every buffer of Ub
             Ub[(i / pad) * G::P2 + G::nS * R + i % pad] = E(0.0f);
     }
     commit_step(0, 0);
@@ -756,7 +773,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         *reinterpret_cast<E4 *>(dst) = h;
     };
     // stage 1 on the x slice in xs (a buffer of Xs)
-    auto stage1 = [&](const E *xs) {
+    auto stage1 = [&](const E *xs, E *ub) {
         // stage 1: U^T = F . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]. A tile (mt, nt) stores at
         // ub_tile(mt, nt) + ub_lane: the rows (f, r1, r2) of mt*16 + 4*lgrp and the columns
         // (iL', t, iS) of nt*16 + lrow split into tile and lane parts (R and 16 are powers of
@@ -769,17 +786,17 @@ __global__ void __launch_bounds__(Geo<C>::NT)
 #pragma unroll
                 for (int i = 0; i < G::BM1; ++i) {
                     const int mt = wave * G::BM1 + i;
-                    if (G::M1T % G::NW == 0 || mt < G::M1T) put4(Ub + ub_lane + ub_tile(mt, nt), d[i]);
+                    if (G::M1T % G::NW == 0 || mt < G::M1T) put4(ub + ub_lane + ub_tile(mt, nt), d[i]);
                 }
             });
         } else {
             lds_gemm<O, G::M1T, G::N1T, G::KF, G::PF, G::NW>(Fs, xs, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
                 if (G::nS % 16 == 0 || (nt % (G::nSP / 16)) * 16 + lrow < G::nS)
-                    put4(Ub + ub_lane + ub_tile(mt, nt), d);
+                    put4(ub + ub_lane + ub_tile(mt, nt), d);
             });
         }
     };
-    auto stage2 = [&]() {
+    auto stage2 = [&](const E *ub, E *vb) {
         // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)], rows (s, r3) of mt*16 + 4*lgrp
         // and columns (iL', r1, t, f) of nt*16 + lrow split into tile and lane parts alike
         if constexpr (G::W32) {
@@ -791,39 +808,39 @@ __global__ void __launch_bounds__(Geo<C>::NT)
 #pragma unroll
                     for (int g = 0; g < 4; ++g)
                         if (G::M2 % (32 * G::WM2) == 0 || mt * 32 + 8 * g + 4 * (lane >> 5) < G::M2)
-                            put4(Vb + vb_lane32 + vb_tile32(mt, nt) + vb_row(8 * g),
+                            put4(vb + vb_lane32 + vb_tile32(mt, nt) + vb_row(8 * g),
                                  f32x4{d[i][4 * g], d[i][4 * g + 1], d[i][4 * g + 2], d[i][4 * g + 3]});
                 }
             };
             if constexpr (G::TAIL) {
                 if (wave < HW)
-                    reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, 1>(sa, Ub, 0, lane, st);
+                    reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, 1>(sa, ub, 0, lane, st);
                 else
-                    reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, G::TAILJ>(sa, Ub, wn2, lane, st);
+                    reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, G::TAILJ>(sa, ub, wn2, lane, st);
             } else if (G::M2T32 % G::WM2 == 0 || wm2 * G::BM2 < G::M2T32) {  // else no rows
-                reg_gemm32<O, G::BM2, G::K2, G::P2, G::N2T32, G::WN2>(sa, Ub, wn2, lane, st);
+                reg_gemm32<O, G::BM2, G::K2, G::P2, G::N2T32, G::WN2>(sa, ub, wn2, lane, st);
             }
         } else if constexpr (G::WIDE) {
             if (G::M2T % G::WM2 == 0 || wm2 * G::BM2 < G::M2T)  // else this wave has no rows
-            reg_gemm<O, G::BM2, G::K2, G::P2, G::N2T, G::WN2>(sa, Ub, wn2, lrow, lgrp, [&](int nt, const f32x4 *d) {
+            reg_gemm<O, G::BM2, G::K2, G::P2, G::N2T, G::WN2>(sa, ub, wn2, lrow, lgrp, [&](int nt, const f32x4 *d) {
                 if (G::N2 % 16 != 0 && nt * 16 + lrow >= G::N2) return;
 #pragma unroll
                 for (int i = 0; i < G::BM2; ++i) {
                     const int mt = wm2 * G::BM2 + i;
                     if (G::M2 % (16 * G::WM2) == 0 || mt * 16 + 4 * lgrp < G::M2)
-                        put4(Vb + vb_lane + vb_tile(mt, nt), d[i]);
+                        put4(vb + vb_lane + vb_tile(mt, nt), d[i]);
                 }
             });
         } else {
-            lds_gemm<O, G::M2T, G::N2T, G::K2, G::P2, G::NW>(Ss, Ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
+            lds_gemm<O, G::M2T, G::N2T, G::K2, G::P2, G::NW>(Ss, ub, wave, lrow, lgrp, [&](int mt, int nt, f32x4 d) {
                 if ((G::N2 % 16 == 0 || nt * 16 + lrow < G::N2) &&
                     (G::M2 % 16 == 0 || mt * 16 + 4 * lgrp < G::M2))
-                    put4(Vb + vb_lane + vb_tile(mt, nt), d);
+                    put4(vb + vb_lane + vb_tile(mt, nt), d);
             });
         }
     };
     // stage 3 on the last-core slice in ls (a buffer of Ls)
-    auto stage3 = [&](const E *ls) {
+    auto stage3 = [&](const E *vb, const E *ls) {
         // stage 3: Y[(t,f,s), l] += Vb . Ls; each wave of a group takes PERK of the K steps,
         // reading the fragments of QB steps before running their MFMAs
         constexpr int QB = PERK < 16 ? PERK : 16;
@@ -833,7 +850,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             const int tile = g3 + G::G3 * j;
             if (G::NT3 % G::G3 == 0 || tile < G::NT3) {
                 const int mt = tile / G::N3T, nt = tile % G::N3T;
-                const E *a = Vb + (mt * 16 + lrow) * G::P3;
+                const E *a = vb + (mt * 16 + lrow) * G::P3;
                 const int l = nt * 16 + lrow;
 #pragma unroll
                 for (int q0 = 0; q0 < PERK; q0 += QB) {
@@ -853,7 +870,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         }
     };
 
-    if constexpr (C.PIPE) {
+    if constexpr (C.PIPE == 1) {
         // Two buffers of Ls and Xs. Step k+1's slices are committed while step k's are still
         // being read, and stage 3 of step k runs in the same barrier interval as stage 1 of
         // step k+1 (they touch disjoint buffers: Vb and Ls[k] against Xs[k+1] and Ub), so a
@@ -864,18 +881,49 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         // Buffer (k+1)&1 was last read by stage 3(k-1) and stage 1(k-1), both before the
         // second barrier of step k-1.
         issue_step(G::IC);
-        stage1(Xs);
+        stage1(Xs, Ub);
         __syncthreads();
-        stage2();
+        stage2(Ub, Vb);
         for (int step = 0; step < G::NSTEP; ++step) {
             const int next = step + 1;
             if (next < G::NSTEP) commit_step(next * G::IC, next & 1);
             __syncthreads();
             if (next + 1 < G::NSTEP) issue_step((next + 1) * G::IC);
-            stage3(Ls + (step & 1) * G::szLs);
-            if (next < G::NSTEP) stage1(Xs + (next & 1) * G::szXs);
+            stage3(Vb, Ls + (step & 1) * G::szLs);
+            if (next < G::NSTEP) stage1(Xs + (next & 1) * G::szXs, Ub);
             __syncthreads();
-            if (next < G::NSTEP) stage2();
+            if (next < G::NSTEP) stage2(Ub, Vb);
+        }
+    } else if constexpr (C.PIPE == 2) {
+        // Ub and Vb double-buffered as well: barrier interval i holds stage 1 of step i, stage
+        // 2 of step i-1 and stage 3 of step i-2, on disjoint buffers (Xs[i&1] -> Ub[i&1];
+        // Ub[(i-1)&1] -> Vb[(i-1)&1]; Vb[i&1] and Ls[i&1] -> y), one barrier per step. Waves
+        // 0..NW/2-1 take stage 2 first and waves NW/2.. last, so that the two waves sharing a
+        // SIMD overlap one's MFMA-bound stage 2 with the other's LDS-bound stages 1 and 3.
+        // A buffer written in interval i was last read in interval i-1 or i-2, and is read
+        // next in interval i+1 or i+2: the barrier that opens each interval orders them.
+        // x of step i+1 and the last-core slice of step i-1 are loaded during interval i and
+        // committed before the barrier of interval i+1 (the prologue put step 0's slices in
+        // Xs[0] and Ls[0]).
+        for (int i = 0; i < G::NSTEP + 2; ++i) {
+            const bool s1 = i < G::NSTEP, s2 = i >= 1 && i - 1 < G::NSTEP, s3 = i >= 2;
+            if (i >= 1 && i < G::NSTEP) commit_x(i * G::IC, i & 1);
+            if (i >= 3) commit_l(i & 1);  // the slice of step i-2
+            if (i >= 1) __syncthreads();   // interval 0 follows the prologue's barrier
+            if (i + 1 < G::NSTEP) issue_x((i + 1) * G::IC);
+            if (i >= 2 && i - 1 < G::NSTEP) issue_l((i - 1) * G::IC);
+            E *ub_i = Ub + (i & 1) * G::szUb, *ub_p = Ub + ((i - 1) & 1) * G::szUb;
+            E *vb_p = Vb + ((i - 1) & 1) * G::szVb, *vb_i = Vb + (i & 1) * G::szVb;
+            const E *xs_i = Xs + (i & 1) * G::szXs, *ls_i = Ls + (i & 1) * G::szLs;
+            if (wave < G::NW / 2) {
+                if (s2) stage2(ub_p, vb_p);
+                if (s3) stage3(vb_i, ls_i);
+                if (s1) stage1(xs_i, ub_i);
+            } else {
+                if (s3) stage3(vb_i, ls_i);
+                if (s1) stage1(xs_i, ub_i);
+                if (s2) stage2(ub_p, vb_p);
+            }
         }
     } else {
         for (int step = 0; step < G::NSTEP; ++step) {
@@ -888,11 +936,11 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             // prefetch the next step's last-core slice and x into registers; they land while
             // this step computes, so a step pays no memory latency of its own
             if (step + 1 < G::NSTEP) issue_step(iL0 + G::IC);
-            stage1(Xs);
+            stage1(Xs, Ub);
             __syncthreads();
-            stage2();
+            stage2(Ub, Vb);
             __syncthreads();
-            stage3(Ls);
+            stage3(Vb, Ls);
         }
     }
 
@@ -1053,11 +1101,13 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
         if (k.WIDE)
             std::snprintf(v.name, sizeof(v.name),
                           "ring3_mfma_wide%d%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
-                          k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "", k.PIPE ? "p" : "", k.F,
+                          k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "",
+                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         else
             std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
-                          k.NW == 8 ? "_w8" : "", k.PIPE ? "_p" : "", k.F, k.S, k.L, k.TT, k.FC,
+                          k.NW == 8 ? "_w8" : "", k.PIPE == 2 ? "_p2" : k.PIPE ? "_p" : "", k.F,
+                          k.S, k.L, k.TT, k.FC,
                           k.SC, k.LC, k.IC, k.KS3, k.NACC);
         ++added;
     }

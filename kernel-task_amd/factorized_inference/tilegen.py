@@ -83,7 +83,8 @@ class Tile:
     WIDE: int = 0
     MF2: int = 16
     NW: int = 4
-    PIPE: int = 0  # double-buffered last-core and x slices, two barriers per step
+    PIPE: int = 0  # 1: double-buffered slices, two barriers per step; 2: also double-buffered
+    #                stage results, three steps' stages in one barrier interval
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
@@ -210,14 +211,14 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     BM1 = cdiv(M1T, NW)
     BM2 = cdiv(M2T32 if W32 else M2T, WM2)
     N2R = N2T32 * 32 if W32 else N2P
-    nbuf = 2 if t.PIPE else 1
+    nbuf, nbuf2 = (2 if t.PIPE else 1), (2 if t.PIPE == 2 else 1)
     sz = {
         "Fs": 8 if wide else M1 * PF,
         "Ss": 8 if wide else M2P * P2,
         "Ls": nbuf * t.IC * LCP * PL,
         "Xs": nbuf * N1 * PF,
-        "Ub": N2R * P2,
-        "Vb": M3P * P3,
+        "Ub": nbuf2 * N2R * P2,
+        "Vb": nbuf2 * M3P * P3,
     }
     lds = 2 * sum(sz.values())
     red_floats = (t.KS3 - 1) * G3 * NYW * 256
@@ -244,10 +245,10 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (t.FC <= c.oF and t.SC <= c.oS and t.LC <= c.oL and t.IC <= c.nL and t.TT >= 1,
          "tile too large"),
         (c.nL % t.IC == 0, "IC must divide the last core's input mode"),
-        (t.PIPE in (0, 1) and (t.PIPE == 0 or c.nL // t.IC > 1), "a pipelined tile needs two steps"),
+        (t.PIPE in (0, 1, 2) and (t.PIPE == 0 or c.nL // t.IC > 1), "a pipelined tile needs two steps"),
         (c.xrow or c.IN % 8 == 0, "scatter loader reads x rows in 8-element vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
-        (red_floats * 4 <= sz["Ub"] * 2, "stage-3 reduction does not fit in Ub"),
+        (red_floats * 4 <= N2R * P2 * 2, "stage-3 reduction does not fit in Ub"),
         (not wide or g["slice_vgprs"] <= WIDE_VGPR_RELAXED[NW],
          "register-resident slices too large"),
     ]
@@ -364,12 +365,13 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
                     t = Tile(tt, 1, base.SC, LC, ic, ks3, nacc, wide, 32, nw)
                     if not geometry(shape, order, t)["reject"] and t not in out.values():
                         out[f"{fam}_t{tt}k{ks3}n{nacc}_ic{ic}"] = t
-        # the pipelined main loop for every multi-step tile found so far that still fits
+        # the pipelined main loops for every multi-step tile found so far that still fits
         for name, t in list(out.items()):
             if cdiv(c.nL, t.IC) > 1:
-                p = replace(t, PIPE=1)
-                if not geometry(shape, order, p)["reject"] and p not in out.values():
-                    out[name + "_p"] = p
+                for pipe, tag in ((1, "_p"), (2, "_p2")):
+                    p = replace(t, PIPE=pipe)
+                    if not geometry(shape, order, p)["reject"] and p not in out.values():
+                        out[name + tag] = p
     if not any(n.startswith("wide") for n in out):
         # no register-resident tile within the budget (a long stage-2 K): offer the smallest
         # over-budget one, which may spill a few registers; the autotuner decides
@@ -380,7 +382,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
     return out
 
 
-_VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p)?|(_w8)?(_p)?)<(\d)(\d)(\d),"
+_VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?|(_w8)?(_p2?)?)<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -392,9 +394,10 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     wide = int(m.group(1) or 0)
     order = tuple(int(m.group(i)) for i in (7, 8, 9))
     TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(10, 17))
+    pipe_tag = m.group(4) or m.group(6) or ""
+    pipe = 2 if pipe_tag.endswith("2") else 1 if pipe_tag else 0
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
-                       8 if (m.group(3) or m.group(5)) else 4,
-                       1 if (m.group(4) or m.group(6)) else 0)
+                       8 if (m.group(3) or m.group(5)) else 4, pipe)
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:

@@ -42,6 +42,9 @@ def test_variant_names_parse_back_to_their_tiles():
     assert parse("ring3_mfma_w8_p<210,1,1,1,12,4,8,1>")[1] == tilegen.Tile(
         1, 1, 1, 12, 4, 8, 1, 0, 16, 8, 1)
     assert parse("ring3_mfma_p<210,1,1,10,12,2,1,2>")[1].PIPE == 1
+    assert parse("ring3_mfma_p2<210,1,1,10,12,2,1,2>")[1].PIPE == 2
+    assert parse("ring3_mfma_wide8x32w8p2<210,2,1,16,16,1,1,2>")[1] == tilegen.Tile(
+        2, 1, 16, 16, 1, 1, 2, 8, 32, 8, 2)
     with pytest.raises(ValueError):
         parse("ring3_generic<012,rc=8>")
 
