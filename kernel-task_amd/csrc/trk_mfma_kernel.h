@@ -43,6 +43,11 @@ namespace trk {
 namespace {
 
 using f32x4 = float __attribute__((ext_vector_type(4)));
+
+// The kernel body's helper lambdas capture register arrays (prefetched slices, accumulators)
+// by reference: one that the compiler leaves as a call puts those arrays in scratch memory
+// (measured: a 3.5x slower tile), so every one is inlined.
+#define TRK_INLINE __attribute__((always_inline))
 using f32x16 = float __attribute__((ext_vector_type(16)));
 
 template <int DT>
@@ -608,7 +613,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     // contiguous-iF loader: vector v of the step covers Xs[n][c*VX, c*VX+VX) of row
     // n = (iL', t, iS); what lies outside x (K padding, iS >= nS, absent tokens) is zero, so
     // these vectors write every element of Xs[:, 0:KF)
-    auto x_row_load = [&](int v, int iL0) {
+    auto x_row_load = [&](int v, int iL0) TRK_INLINE {
         const int n = v / G::XCPR, c = v % G::XCPR;
         const int iS = n % G::nSP, t = (n / G::nSP) % G::TT, iL = iL0 + n / (G::nSP * G::TT);
         XV r{};
@@ -618,13 +623,13 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                                               iL * G::SXL + c * G::VX);
         return r;
     };
-    auto x_scatter_load = [&](int v) {       // scatter loader: 8 contiguous x elements
+    auto x_scatter_load = [&](int v) TRK_INLINE {       // scatter loader: 8 contiguous x elements
         uint4 r = make_uint4(0u, 0u, 0u, 0u);
         if (v < G::NXB && t0 + v / (G::IN / 8) < T)
             r = reinterpret_cast<const uint4 *>(x + size_t(t0) * G::IN)[v];
         return r;
     };
-    auto x_scatter_store = [&](int v, uint4 r, int iL0, E *xs) {
+    auto x_scatter_store = [&](int v, uint4 r, int iL0, E *xs) TRK_INLINE {
         const int t = v / (G::IN / 8);
         if (v >= G::NXB || t0 + t >= T) return;
         const E *e = reinterpret_cast<const E *>(&r);
@@ -640,10 +645,10 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT> cF;
     RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8, G::NT> cS;
     RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, G::NT> cL;
-    auto issue_l = [&](int iL0) {  // the last-core slice of the step at input digit iL0
+    auto issue_l = [&](int iL0) TRK_INLINE {  // the last-core slice of the step at input digit iL0
         cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
     };
-    auto issue_x = [&](int iL0) {  // x for the step at input digit iL0
+    auto issue_x = [&](int iL0) TRK_INLINE {  // x for the step at input digit iL0
         if constexpr (G::XROW) {
 #pragma unroll
             for (int j = 0; j < XREG; ++j) xr[j] = x_row_load(tid + j * G::NT, iL0);
@@ -652,15 +657,15 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * G::NT);
         }
     };
-    auto issue_step = [&](int iL0) {
+    auto issue_step = [&](int iL0) TRK_INLINE {
         issue_l(iL0);
         issue_x(iL0);
     };
-    auto commit_l = [&](int buf) {  // into buffer `buf` of Ls
+    auto commit_l = [&](int buf) TRK_INLINE {  // into buffer `buf` of Ls
         wait_loads();
         cL.commit(Ls + buf * G::szLs);
     };
-    auto commit_x = [&](int iL0, int buf) {  // into buffer `buf` of Xs
+    auto commit_x = [&](int iL0, int buf) TRK_INLINE {  // into buffer `buf` of Xs
         E *xs = Xs + buf * G::szXs;
         wait_loads();
         if constexpr (G::XROW) {
@@ -686,7 +691,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             }
         }
     };
-    auto commit_step = [&](int iL0, int buf) {  // into buffer `buf` of Ls and Xs
+    auto commit_step = [&](int iL0, int buf) TRK_INLINE {  // into buffer `buf` of Ls and Xs
         commit_l(buf);
         commit_x(iL0, buf);
     };
@@ -768,12 +773,12 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     constexpr int K3STEPS = G::K3 / 32, PERK = K3STEPS / G::KS3;
     static_assert(K3STEPS % G::KS3 == 0, "stage-3 K steps must split evenly over KS3 waves");
 
-    auto put4 = [&](E *dst, f32x4 d) {
+    auto put4 = [&](E *dst, f32x4 d) TRK_INLINE {
         E4 h = {E(d[0]), E(d[1]), E(d[2]), E(d[3])};
         *reinterpret_cast<E4 *>(dst) = h;
     };
     // stage 1 on the x slice in xs (a buffer of Xs)
-    auto stage1 = [&](const E *xs, E *ub) {
+    auto stage1 = [&](const E *xs, E *ub) TRK_INLINE {
         // stage 1: U^T = F . Xs^T  ->  Ub[(iL',r1,t,f)][(iS,r2)]. A tile (mt, nt) stores at
         // ub_tile(mt, nt) + ub_lane: the rows (f, r1, r2) of mt*16 + 4*lgrp and the columns
         // (iL', t, iS) of nt*16 + lrow split into tile and lane parts (R and 16 are powers of
@@ -796,11 +801,11 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             });
         }
     };
-    auto stage2 = [&](const E *ub, E *vb) {
+    auto stage2 = [&](const E *ub, E *vb) TRK_INLINE {
         // stage 2: V^T = S . Ub^T  ->  Vb[(t,f,s)][(iL',r1,r3)], rows (s, r3) of mt*16 + 4*lgrp
         // and columns (iL', r1, t, f) of nt*16 + lrow split into tile and lane parts alike
         if constexpr (G::W32) {
-            auto st = [&](int nt, const f32x16 *d) {
+            auto st = [&](int nt, const f32x16 *d) TRK_INLINE {
                 if (G::N2 % 32 != 0 && nt * 32 + (lane & 31) >= G::N2) return;
 #pragma unroll
                 for (int i = 0; i < G::BM2; ++i) {
@@ -840,7 +845,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         }
     };
     // stage 3 on the last-core slice in ls (a buffer of Ls)
-    auto stage3 = [&](const E *vb, const E *ls) {
+    auto stage3 = [&](const E *vb, const E *ls) TRK_INLINE {
         // stage 3: Y[(t,f,s), l] += Vb . Ls; each wave of a group takes PERK of the K steps,
         // reading the fragments of QB steps before running their MFMAs
         constexpr int QB = PERK < 16 ? PERK : 16;

@@ -7,7 +7,9 @@ is never built lazily at import or call time (a missing library is an error).
 """
 from __future__ import annotations
 
+import json
 import os
+import re
 import subprocess
 import sys
 import sysconfig
@@ -21,6 +23,8 @@ LIBRARY = PACKAGE / "libtrk.so"
 FASTCALL = PACKAGE / ("_trkcall" + sysconfig.get_config_var("EXT_SUFFIX"))
 TORCHCALL = PACKAGE / ("_trktorch" + sysconfig.get_config_var("EXT_SUFFIX"))
 OBJ_DIR = PACKAGE.parent / "_build"
+# per-kernel register, scratch and LDS use reported by the compiler (a build artifact)
+RESOURCES = PACKAGE / "kernel_resources.json"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no packed fp32 VALU ops (v_pk_*_f32) anywhere in the device code.
@@ -71,19 +75,26 @@ def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Pa
 
     def compile_one(src: Path) -> Path:
         obj = OBJ_DIR / (src.stem + ".o")
-        if (incremental and obj.exists()
+        report = obj.with_suffix(".resources.json")
+        if (incremental and obj.exists() and report.exists()
                 and obj.stat().st_mtime > max(_newest_dependency(), src.stat().st_mtime)):
             return obj
-        cmd = [hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []),
+               "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         done = subprocess.run(cmd, capture_output=True, text=True)
         if done.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src.name}:\n{done.stderr}")
+        report.write_text(json.dumps(parse_resource_remarks(done.stderr)))
         return obj
 
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
         objects = list(pool.map(compile_one, sources()))
+    resources = {}
+    for obj in objects:
+        resources.update(json.loads(obj.with_suffix(".resources.json").read_text()))
+    RESOURCES.write_text(json.dumps(resources, indent=0, sort_keys=True) + "\n")
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objects)]
@@ -100,6 +111,23 @@ def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Pa
     subprocess.run(cmd, check=True)
     _build_torchcall(verbose)
     return LIBRARY
+
+
+_REMARK = re.compile(r"remark: +(Function Name|[A-Za-z][A-Za-z /]*?)(?: \[[^\]]*\])?: (\S+) "
+                     r"\[-Rpass-analysis=kernel-resource-usage\]")
+
+
+def parse_resource_remarks(stderr: str) -> dict[str, dict[str, str]]:
+    """{kernel: {"VGPRs": .., "AGPRs": .., "ScratchSize": .., "VGPRs Spill": .., ...}} from the
+    compiler's kernel-resource-usage remarks (device pass only; host remarks do not occur)."""
+    out: dict[str, dict[str, str]] = {}
+    current = None
+    for key, value in _REMARK.findall(stderr):
+        if key == "Function Name":
+            current = out.setdefault(value, {})
+        elif current is not None:
+            current[key.strip()] = value
+    return out
 
 
 def _build_torchcall(verbose: bool) -> None:
