@@ -60,10 +60,16 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
     dtype = getattr(torch, dtype_name)
     spec = TRSpec(ins, outs, rank)
     cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init=init)
+    m.synchronize()
+    mem0 = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
     t0 = time.perf_counter()
     run = prepare_optimized(cores, spec)
     m.synchronize()
     prep_ms = (time.perf_counter() - t0) * 1e3
+    # device memory: what preparing holds (the packed cores) and its transient peak
+    prep_held = torch.cuda.memory_allocated() - mem0
+    prep_peak = torch.cuda.max_memory_allocated() - mem0
     weight = materialize_dense_weight(cores, spec)
     results = []
     for T in tokens:
@@ -72,7 +78,10 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
         ours = lambda: run(x)  # noqa: E731
         dense = lambda: dense_forward(x, weight)  # noqa: E731
         one = m.host_us(ours, 1)[0]              # first call; sizes the loops below
-        warm = max(2, min(warmup, int(0.2e6 / max(one, 1.0))))
+        # the headline takes exactly W untimed steps; the other cases warm up for ~0.3 s of
+        # calls (the GPU clock takes a few hundred ms of load to settle; 20 calls of a 30 us
+        # kernel measured 10 % slow)
+        warm = warmup if headline and T == 1 else max(warmup, min(20000, int(0.3e6 / max(one, 1.0))))
         for _ in range(warm):
             ours()
             dense()
@@ -91,8 +100,15 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
         host_ours = statistics.median(m.host_us(ours, min(50, calls)))
         host_dense = statistics.median(m.host_us(dense, 50))
         submit_us = m.host_submit_us(ours, min(200, calls))
+        # device memory of one call beyond its output: nothing (no workspace, no counters)
+        m.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        y = run(x)
+        m.synchronize()
+        call_extra = torch.cuda.max_memory_allocated() - base - y.numel() * y.element_size()
         # correctness after timing, against the fp32 factorized path on the same cores
-        y = run(x).float()
+        y = y.float()
         ref = tr_forward_reference(x.float(), [c.float() for c in cores], spec)
         err = (y - ref).abs().max().item()
         info = run.selected(T)
@@ -105,7 +121,10 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
             "ours_host_us": host_ours, "dense_host_us": host_dense, "ours_submit_us": submit_us,
             "flops": info["flops"], "bytes": info["bytes"],
             "max_abs_err_vs_fp32": err, "max_abs_ref": ref.abs().max().item(),
-            "prepare_ms": prep_ms,
+            "prepare_ms": prep_ms, "packed_bytes": run.packed_bytes,
+            "prepare_held_bytes": prep_held, "prepare_peak_bytes": prep_peak,
+            "call_extra_bytes": call_extra,
+            "dense_weight_bytes": weight.numel() * weight.element_size(),
             **m.roofline(info["flops"], info["bytes"], ours_us, dtype),
         }
         log(f"{label} T={T}: ours {ours_us:.2f} us, dense {dense_us:.2f} us, "
@@ -207,6 +226,14 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
     torch.set_num_threads(1)
     with torch.inference_mode():
+        # bring the GPU to its working clock before the first case (dense GEMMs, untimed)
+        a = torch.randn(4096, 4096, device="cuda", dtype=torch.float16)
+        t_end = time.perf_counter() + 0.5
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                a @ a
+            torch.cuda.synchronize()
+        del a
         cases = []
         for i, (label, ins, outs, rank, dt, init, tokens) in enumerate(CASES):
             if args.headline_only and i > 0:

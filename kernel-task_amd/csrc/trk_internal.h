@@ -10,7 +10,7 @@
 
 namespace trk {
 
-constexpr int kMaxVariants = 192;  // an autotuning build compiles up to ~130 tiles per shape
+constexpr int kMaxVariants = 256;  // an autotuning build compiles up to ~180 tiles per shape
 constexpr int kMaxChains = 6;
 
 // One contraction order, in chain terms. The cores are re-indexed as chain cores

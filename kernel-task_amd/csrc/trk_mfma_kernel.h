@@ -112,6 +112,8 @@ struct KCfg {
                              // (two barriers per step instead of four); 2: the stage results
                              // (Ub, Vb) are double-buffered too, and stages 1, 2 and 3 of three
                              // consecutive steps share one barrier interval; 0: one buffer
+    int S1;                  // WIDE stage 1: row tiles per wave (the waves split the columns
+                             // NW * S1 / M1T ways); 0: the default split (below)
 };
 
 template <KCfg C>
@@ -163,7 +165,14 @@ struct Geo {
     static constexpr int WM2 = WIDE ? C.WIDE : NW, WN2 = NW / WM2;
     static constexpr bool W32 = WIDE && C.MF2 == 32;  // stage 2 on 32x32 tiles
     static constexpr int M2T32 = cdiv(M2, 32), N2T32 = cdiv(N2, 32);
-    static constexpr int BM1 = cdiv(M1T, NW), BM2 = cdiv(W32 ? M2T32 : M2T, WM2);
+    // WIDE stage 1 on a WM1 x WN1 grid of waves (row groups of BM1 tiles x column phases).
+    // By default every wave takes its own rows and all columns, or, with fewer row tiles than
+    // waves, one row tile and a share of the columns (no wave idles); S1 sets larger row
+    // groups, which read the x slice from LDS fewer times at the cost of registers.
+    static constexpr int BM1 = C.S1 ? C.S1 : M1T < NW && NW % M1T == 0 ? 1 : cdiv(M1T, NW);
+    static constexpr int WM1 = C.S1 || (M1T < NW && NW % M1T == 0) ? M1T / BM1 : NW;
+    static constexpr int WN1 = NW / WM1;
+    static constexpr int BM2 = cdiv(W32 ? M2T32 : M2T, WM2);
     static constexpr int N2R = W32 ? N2T32 * 32 : N2P;  // Ub rows (the last tile's padding)
     // W32 with one row tile per wave and fewer row tiles than waves (8): waves 0-3 take a row
     // tile each and waves 4-7 split the TAILR remaining row tiles' columns TAILJ ways. Waves
@@ -209,6 +218,8 @@ struct Geo {
     static_assert(C.PIPE >= 0 && C.PIPE <= 2 && (C.PIPE == 0 || NSTEP > 1),
                   "a pipelined tile needs two steps");
     static_assert(XROW || IN % 8 == 0, "scatter loader reads x rows in 8-element vectors");
+    static_assert(C.S1 == 0 || (WIDE && M1T % C.S1 == 0 && NW % (M1T / C.S1) == 0),
+                  "S1 must split the stage-1 rows into a divisor of the waves");
 };
 
 
@@ -599,8 +610,11 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     const int s0 = (b % G::NSC) * G::SC;
     const int f0 = (b / G::NSC) * G::FC;
     const int t0 = blockIdx.y * G::TT;
-    const int FCv = min(G::FC, G::oF - f0), SCv = min(G::SC, G::oS - s0);
-    const int LCv = min(G::LC, G::oL - l0);
+    // digits of each core this workgroup owns: compile-time constants when the chunks divide
+    // the modes, which removes the bounds branches around the slice loads
+    const int FCv = G::oF % G::FC == 0 ? G::FC : min(G::FC, G::oF - f0);
+    const int SCv = G::oS % G::SC == 0 ? G::SC : min(G::SC, G::oS - s0);
+    const int LCv = G::oL % G::LC == 0 ? G::LC : min(G::LC, G::oL - l0);
 
     // Global -> LDS for one step of IC last-core input digits: the last-core slice and x are
     // read into registers (issue), then written to Ls and Xs[(iL', t, iS)][iF] (commit).
@@ -696,6 +710,9 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         commit_x(iL0, buf);
     };
 
+    // stage-1 row group and column phase of this wave (WIDE; constants when trivial)
+    const int wm1 = G::WM1 == G::NW ? wave : wave % G::WM1;
+    const int wn1 = G::WN1 == 1 ? 0 : wave / G::WM1;
     // stage-2 row group and column phase of this wave (WIDE)
     constexpr int HW = G::NW / 2;
     const int wm2 = G::TAIL ? (wave < HW ? wave : HW + (wave - HW) / G::TAILJ) : wave % G::WM2;
@@ -704,7 +721,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     RegA<O, G::BM1, G::KF> fa;
     std::conditional_t<G::W32, RegA32<O, G::BM2, G::K2>, RegA<O, G::BM2, G::K2>> sa;
     if constexpr (G::WIDE) {
-        fa.load(Fk + size_t(f0) * R2 * G::KF, wave * G::BM1 * 16, FCv * R2, lrow, lgrp);
+        fa.load(Fk + size_t(f0) * R2 * G::KF, wm1 * G::BM1 * 16, FCv * R2, lrow, lgrp);
         if constexpr (G::W32)
             sa.load(Sk + size_t(s0) * R * G::K2, wm2 * G::BM2 * 32, SCv * R, lane);
         else
@@ -785,13 +802,14 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         // two and nSP is a multiple of 16, so no part carries into another).
         if constexpr (G::WIDE) {
             // a wave whose row tiles all lie past the last one has no stage-1 work
-            if (G::M1T % G::NW == 0 || wave * G::BM1 < G::M1T)
-            reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T, 1>(fa, xs, 0, lrow, lgrp, [&](int nt, const f32x4 *d) {
+            if (G::M1T % (G::WM1 * G::BM1) == 0 || wm1 * G::BM1 < G::M1T)
+            reg_gemm<O, G::BM1, G::KF, G::PF, G::N1T, G::WN1>(fa, xs, wn1, lrow, lgrp, [&](int nt, const f32x4 *d) {
                 if (G::nS % 16 != 0 && (nt % (G::nSP / 16)) * 16 + lrow >= G::nS) return;
 #pragma unroll
                 for (int i = 0; i < G::BM1; ++i) {
-                    const int mt = wave * G::BM1 + i;
-                    if (G::M1T % G::NW == 0 || mt < G::M1T) put4(ub + ub_lane + ub_tile(mt, nt), d[i]);
+                    const int mt = wm1 * G::BM1 + i;
+                    if (G::M1T % (G::WM1 * G::BM1) == 0 || mt < G::M1T)
+                        put4(ub + ub_lane + ub_tile(mt, nt), d[i]);
                 }
             });
         } else {
@@ -1069,9 +1087,9 @@ struct Shape {
     int dt, F, S, L, i0, i1, i2, o0, o1, o2, R;
 };
 constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
-                    int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0) {
+                    int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0, int S1 = 0) {
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
-                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE};
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1};
 }
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>},
@@ -1103,17 +1121,20 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
         v.t_min = e.t_min;
         v.t_max = e.t_max;
         v.launch = e.launch;
-        if (k.WIDE)
+        if (k.WIDE) {
+            char s1[8] = "";
+            if (k.S1) std::snprintf(s1, sizeof(s1), "_s%d", k.S1);
             std::snprintf(v.name, sizeof(v.name),
-                          "ring3_mfma_wide%d%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
+                          "ring3_mfma_wide%d%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
                           k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "",
-                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", k.F,
+                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
-        else
+        } else {
             std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
                           k.NW == 8 ? "_w8" : "", k.PIPE == 2 ? "_p2" : k.PIPE ? "_p" : "", k.F,
                           k.S, k.L, k.TT, k.FC,
                           k.SC, k.LC, k.IC, k.KS3, k.NACC);
+        }
         ++added;
     }
     return added;

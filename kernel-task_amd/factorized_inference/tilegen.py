@@ -85,14 +85,17 @@ class Tile:
     NW: int = 4
     PIPE: int = 0  # 1: double-buffered slices, two barriers per step; 2: also double-buffered
     #                stage results, three steps' stages in one barrier interval
+    S1: int = 0    # WIDE stage-1 row tiles per wave (0: the kernel's default split)
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
         a = [self.TT, self.FC, self.SC, self.LC, self.IC, self.KS3, self.NACC]
         if (self.WIDE, self.MF2, self.NW, self.PIPE) != (0, 16, 4, 0):
             a += [self.WIDE, self.MF2, self.NW]
-        if self.PIPE:
+        if self.PIPE or self.S1:
             a.append(self.PIPE)
+        if self.S1:
+            a.append(self.S1)
         return ", ".join(map(str, a))
 
 
@@ -208,7 +211,12 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     NYW = cdiv(NT3, G3)
     PF, P2, P3, PL = KF + 8, K2 + 8, K3 + 8, R2 + 8
     M2T32, N2T32 = cdiv(M2, 32), cdiv(N2, 32)
-    BM1 = cdiv(M1T, NW)
+    if t.S1:
+        BM1, WM1 = t.S1, M1T // t.S1 if M1T % t.S1 == 0 else 0
+    elif M1T < NW and NW % M1T == 0:
+        BM1, WM1 = 1, M1T
+    else:
+        BM1, WM1 = cdiv(M1T, NW), NW
     BM2 = cdiv(M2T32 if W32 else M2T, WM2)
     N2R = N2T32 * 32 if W32 else N2P
     nbuf, nbuf2 = (2 if t.PIPE else 1), (2 if t.PIPE == 2 else 1)
@@ -229,8 +237,10 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
              NSTEP=cdiv(c.nL, t.IC), BM1=BM1, BM2=BM2, NYW=NYW, K2=K2, KF=KF)
     # register-resident slices (WIDE): A fragments held by each wave
     if wide:
-        fa = BM1 * (KF // 32 * 4 + (2 if KF % 32 else 0))
-        sa = BM2 * (K2 // 16) * 4 if W32 else BM2 * (K2 // 32 * 4 + (2 if K2 % 32 else 0))
+        # a trailing 16 of K after 32-wide steps is held as a full 8-element fragment
+        tail = lambda k: (4 if k >= 32 else 2) if k % 32 else 0  # noqa: E731
+        fa = BM1 * (KF // 32 * 4 + tail(KF))
+        sa = BM2 * (K2 // 16) * 4 if W32 else BM2 * (K2 // 32 * 4 + tail(K2))
         g["slice_vgprs"] = fa + sa
     checks = [
         (R % 8 == 0 and R & (R - 1) == 0, "rank must be a power of two >= 8"),
@@ -246,6 +256,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
          "tile too large"),
         (c.nL % t.IC == 0, "IC must divide the last core's input mode"),
         (t.PIPE in (0, 1, 2) and (t.PIPE == 0 or c.nL // t.IC > 1), "a pipelined tile needs two steps"),
+        (t.S1 == 0 or (wide and WM1 > 0 and NW % WM1 == 0), "S1 must split the stage-1 rows"),
         (c.xrow or c.IN % 8 == 0, "scatter loader reads x rows in 8-element vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= N2R * P2 * 2, "stage-3 reduction does not fit in Ub"),
@@ -382,7 +393,8 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
     return out
 
 
-_VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?|(_w8)?(_p2?)?)<(\d)(\d)(\d),"
+_VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?(?:_s(\d+))?|(_w8)?(_p2?)?)"
+                           r"<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -392,12 +404,12 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     if not m:
         raise ValueError(f"not an MFMA variant name: {name!r}")
     wide = int(m.group(1) or 0)
-    order = tuple(int(m.group(i)) for i in (7, 8, 9))
-    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(10, 17))
-    pipe_tag = m.group(4) or m.group(6) or ""
+    order = tuple(int(m.group(i)) for i in (8, 9, 10))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(11, 18))
+    pipe_tag = m.group(4) or m.group(7) or ""
     pipe = 2 if pipe_tag.endswith("2") else 1 if pipe_tag else 0
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
-                       8 if (m.group(3) or m.group(5)) else 4, pipe)
+                       8 if (m.group(3) or m.group(6)) else 4, pipe, int(m.group(5) or 0))
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
@@ -425,6 +437,22 @@ def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
 
 def load_tuned() -> dict:
     return json.loads(TUNED.read_text()) if TUNED.exists() else {}
+
+
+def s1_variants(shape: ShapeDecl, order: tuple, t: Tile) -> dict[str, Tile]:
+    """A register-resident tile with larger stage-1 row groups than the kernel's default split
+    (fewer reads of the x slice from LDS, more registers), every one the kernel accepts."""
+    out = {}
+    if not t.WIDE or t.S1:
+        return out
+    m1t = t.FC * shape.rank * shape.rank // 16
+    default = 1 if m1t < t.NW and t.NW % m1t == 0 else cdiv(m1t, t.NW)
+    for s1 in (2, 4, 8, 16):
+        if s1 > default and m1t % s1 == 0 and t.NW % (m1t // s1) == 0:
+            v = replace(t, S1=s1)
+            if not geometry(shape, order, v)["reject"]:
+                out[f"_s{s1}"] = v
+    return out
 
 
 def search_candidates(shape: ShapeDecl, extended: bool = False) -> dict[str, tuple[tuple, Tile]]:
@@ -458,18 +486,26 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
     cands = search_candidates(shape, extended)
     ranges = rule_ranges([n for n, (o, _) in cands.items() if o == first])
     if all_candidates and shape.key in tuned:
-        # the previous winners stay candidates, so a new search never loses a tile it had
+        # the previous winners stay candidates, so a new search never loses a tile it had;
+        # an extended search also tries their larger stage-1 row groups (a local refinement)
         entry = tuned[shape.key]
         for r in entry["ranges"]:
             order = tuple(r.get("order", entry["order"]))
             if order not in ORDERS:
                 continue
-            key = (order, Tile(**r["tile"]))
-            if key not in cands.values():
-                name = r["name"]
-                if order != first and "@" not in name:
-                    name += "@" + order_tag(order)
-                cands[name] = key
+            tile = Tile(**r["tile"])
+            name = r["name"]
+            if order != first and "@" not in name:
+                name += "@" + order_tag(order)
+            base, _, tag = name.partition("@")
+            tag = "@" + tag if tag else ""
+            found = [(name, tile)]
+            if extended:
+                found += [(base + suffix + tag, v)
+                          for suffix, v in s1_variants(shape, order, tile).items()]
+            for n, t in found:
+                if (order, t) not in cands.values():
+                    cands[n] = (order, t)
     return [(n, o, t, *ranges.get(n, (0, 0))) for n, (o, t) in cands.items()]
 
 
