@@ -100,13 +100,13 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
         host_ours = statistics.median(m.host_us(ours, min(50, calls)))
         host_dense = statistics.median(m.host_us(dense, 50))
         submit_us = m.host_submit_us(ours, min(200, calls))
-        # device memory of one call beyond its output: nothing (no workspace, no counters)
+        # device memory of one call beyond its output (y stays allocated): nothing, no
+        # workspace and no counters
         m.synchronize()
-        base = torch.cuda.memory_allocated()
         torch.cuda.reset_peak_memory_stats()
         y = run(x)
         m.synchronize()
-        call_extra = torch.cuda.max_memory_allocated() - base - y.numel() * y.element_size()
+        call_extra = torch.cuda.max_memory_allocated() - torch.cuda.memory_allocated()
         # correctness after timing, against the fp32 factorized path on the same cores
         y = y.float()
         ref = tr_forward_reference(x.float(), [c.float() for c in cores], spec)
