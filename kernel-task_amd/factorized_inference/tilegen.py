@@ -17,6 +17,13 @@ shapes) gets a generated table:
      kernel-task_amd/benchmarks/autotune.py on an MI355X) when they exist, else a rule.
      Once a shape is tuned, only the tiles that won a token range are compiled.
 
+The extended search (--extended, the autotuner's input) widens step 2: further chain orders
+within 15 % of the least padded work, 1-8 tokens per workgroup in every family, quarter and
+eighth second-core tiles, single-token tiles without the stage-3 wave reduction, more
+last-core inputs per step, a 4-row-group register-resident family on 8 waves, the two
+pipelined main loops (PIPE 1 and 2) of every multi-step tile, and larger stage-1 row groups
+(S1) of the previous winners.
+
 Role of the reference's V3G generators (tools/gen_v3g_tilings.py, tools/gen_v3g_tuned.py,
 src/factorized_inference/v3g_tuned.py:4-17): a compiled variant list for the Qwen3.8-27B
 layer shapes (tools/qwen_shapes.py:20-27) and a measured table of the fastest tiling per
@@ -329,7 +336,10 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
                 return t
         return None
 
-    for wide, nw in ((4, 4), (8, 8)):
+    # (4 row groups on 8 waves: two stage-2 row tiles per wave, so each B fragment read from
+    # LDS feeds two MFMAs, with two waves per SIMD; searched in the extended set only)
+    families = ((4, 4), (8, 8)) + (((4, 8),) if extended else ())
+    for wide, nw in families:
         t = wide_tile(wide, nw, WIDE_VGPR_BUDGET[nw])
         if t is not None and t not in out.values():
             out[f"wide{wide}x32" + ("w8" if nw == 8 else "")] = t
@@ -356,7 +366,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
                         1, 1, sc, LC, ic, ks3, 2), ics)
                     if len(out) > before:
                         break
-        for wide, nw in ((4, 4), (8, 8)):
+        for wide, nw in families:
             fam = f"wide{wide}x32" + ("w8" if nw == 8 else "")
             base = out.get(fam)
             if base is None:
