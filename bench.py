@@ -167,7 +167,19 @@ def cpu_baseline(seconds: float) -> dict:
                    f"{n1} calls of oracle/ring_oracle.tr_forward (the reference's three "
                    f"contractions in its order, numpy BLAS) with 1 BLAS thread"),
         "all_cores_value": many, "all_cores": max(out), "all_cores_calls": nmany,
+        "cpu_model": _cpu_model(),
     }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def traffic_probe(calls: int) -> None:
