@@ -167,6 +167,12 @@ int trk_consume_add(const void *h, const float *y, void *out, int dtype, size_t 
 /* Launch floor: one empty kernel on `stream` (tr_ring.cu:1194-1200, empty_launch). */
 int trk_empty_launch(void *stream);
 
+/* Launch floor of a kernel with arguments: one empty kernel on `stream` whose argument list is
+ * that of the forward kernels (56 bytes). No reference counterpart (the reference's floor
+ * kernel takes no arguments): on MI355X the fetch of a launch's kernel arguments is most of
+ * what a tokens=1 call costs, so this is the floor a forward call is measured against. */
+int trk_empty_launch_args(void *stream);
+
 /* Host floor: a call that does nothing (tr_ring.cu:1202, empty_call). */
 int trk_empty_call(void);
 

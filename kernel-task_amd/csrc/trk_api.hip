@@ -47,18 +47,35 @@ void grid_of(const Plan &p, const Variant &v, int tokens, int grid[3]) {
 }
 }  // namespace
 
-// Index of the chain with this order in the plan, adding it (and its packed sections).
-int plan_chain(Plan *p, const int order[3]) {
+// Index of the chain with this order and these K-order groups in the plan, adding it (and
+// the packed sections it does not share with an earlier chain of the same order).
+int plan_chain(Plan *p, const int order[3], int sg, int lg) {
+    auto same_order = [&](const Chain &c) { return std::equal(order, order + 3, c.order); };
     for (int i = 0; i < p->nchains; ++i)
-        if (std::equal(order, order + 3, p->chains[i].order)) return i;
+        if (same_order(p->chains[i]) && p->chains[i].sg == sg && p->chains[i].lg == lg) return i;
     if (p->nchains == kMaxChains) return -1;
     Chain &c = p->chains[p->nchains];
     describe_chain(p->in_modes, p->out_modes, p->rank, order, &c);
+    c.sg = sg;
+    c.lg = lg;
+    c.ownF = c.ownS = c.ownL = 1;
+    // sections whose layout an earlier chain of this order already has are shared
+    for (int i = 0; i < p->nchains; ++i) {
+        const Chain &o = p->chains[i];
+        if (!same_order(o)) continue;
+        if (c.ownF) { c.offF = o.offF; c.ownF = 0; }
+        if (c.ownS && o.sg == sg) { c.offS = o.offS; c.ownS = 0; }
+        if (c.ownL && o.lg == lg) { c.offL = o.offL; c.ownL = 0; }
+    }
     const size_t e = size_t(p->elem);
-    c.offF = p->packed_bytes;
-    c.offS = align256(c.offF + e * size_t(c.oF) * c.R * c.R * c.KF);
-    c.offL = align256(c.offS + e * size_t(c.oS) * c.R * c.K2);
-    p->packed_bytes = align256(c.offL + e * size_t(c.nL) * c.oL * c.R * c.R);
+    auto take = [&](size_t elems) {
+        const size_t off = p->packed_bytes;
+        p->packed_bytes = align256(off + e * elems);
+        return off;
+    };
+    if (c.ownF) c.offF = take(size_t(c.oF) * c.R * c.R * c.KF);
+    if (c.ownS) c.offS = take(size_t(c.oS) * c.R * c.K2);
+    if (c.ownL) c.offL = take(size_t(c.nL) * c.oL * c.R * c.R);
     return p->nchains++;
 }
 
@@ -158,7 +175,7 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     // (stage 1 recomputed per split, the rank^3 stage divided), for token counts too small
     // to fill the GPU with variant 0's workgroups.
     Variant &g = p->variants[0];
-    g.chain = plan_chain(p, kOrders[best]);
+    g.chain = plan_chain(p, kOrders[best], p->rank, p->rank);  // natural K orders
     const Chain &gc = p->chains[g.chain];
     int st = generic_configure(*p, g.chain, gc.oS, &g);
     if (st != TRK_OK) {
@@ -327,6 +344,10 @@ int trk_consume_add(const void *h, const float *y, void *out, int dtype, size_t 
 }
 
 int trk_empty_launch(void *stream) { return launch_empty(static_cast<hipStream_t>(stream)); }
+
+int trk_empty_launch_args(void *stream) {
+    return launch_empty_args(static_cast<hipStream_t>(stream));
+}
 
 int trk_empty_call(void) { return TRK_OK; }
 

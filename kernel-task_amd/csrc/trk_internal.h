@@ -11,16 +11,20 @@
 namespace trk {
 
 constexpr int kMaxVariants = 256;  // an autotuning build compiles up to ~180 tiles per shape
-constexpr int kMaxChains = 6;
+constexpr int kMaxChains = 12;
 
 // One contraction order, in chain terms. The cores are re-indexed as chain cores
 //   Fc[r1][f][iF][r2], Sc[r2][s][iS][r3], Lc[r3][l][iL][r1]
 // (r1 = link L-F, r2 = link F-S, r3 = link S-L). A forward order follows the ring
 // (G1 -> G2 -> G3 up to rotation) and keeps every core as it is; a backward order swaps the
-// two ring indices of every core. In the packed buffer each chain owns three sections:
+// two ring indices of every core. In the packed buffer each chain has three sections:
 //   Fk[f][r1][r2][KF]  (iF fastest, zero-padded to KF)    first core, stage-1 operand
-//   Sk[s][r3][K2]      (k = iS*R + r2, zero-padded to K2) second core, stage-2 operand
-//   Lk[iL][l][r1][r3]                                    last core, stage-3 operand
+//   Sk[s][r3][K2]      (k = (r2/sg)*sg*nS + iS*sg + r2%sg, zero-padded to K2)
+//                                                        second core, stage-2 operand
+//   Lk[iL][l][K]       (K = (r3/lg)*lg*R + r1*lg + r3%lg) last core, stage-3 operand
+// The K-order groups sg and lg equal R for the natural orders (iS, r2) and (r1, r3) (the
+// generic kernel) and are smaller for the MFMA kernels, whose result stores they make
+// bank-conflict free. Chains of one order share the sections whose layout agrees.
 struct Chain {
     int order[3];    // F, S, L: core indices
     int forward;     // 1 if the order follows the ring
@@ -28,9 +32,11 @@ struct Chain {
     int oF, oS, oL;  // output modes of F, S, L
     int R;
     int KF, K2;      // padded stage-1 and stage-2 contraction lengths
+    int sg, lg;      // K-order groups of the Sk and Lk sections
     int sxF, sxS, sxL;  // element strides of iF, iS, iL in a row of x
     int syF, syS, syL;  // element strides of f, s, l in a row of y
     size_t offF, offS, offL;  // byte offsets of Fk, Sk, Lk in the packed buffer
+    int ownF, ownS, ownL;     // 1 where this chain is the first with that section (packs it)
 };
 
 struct Plan;
@@ -76,8 +82,8 @@ int check_hip(hipError_t err, const char *what);
 // chain geometry (trk_api.hip)
 void describe_chain(const int in_modes[3], const int out_modes[3], int rank, const int order[3],
                     Chain *chain);
-// index of the plan's chain with this order, added with its packed sections if new (-1: full)
-int plan_chain(Plan *plan, const int order[3]);
+// index of the plan's chain with this order and K-order groups, added if new (-1: full)
+int plan_chain(Plan *plan, const int order[3], int sg, int lg);
 
 // kernels and their launchers
 int launch_pack(const Plan &plan, const void *g1, const void *g2, const void *g3, void *packed,
@@ -87,6 +93,7 @@ int generic_configure(const Plan &plan, int chain, int sg, Variant *v);  // trk_
 int launch_generic(const Plan &plan, const Variant &v, const void *packed, const void *x,
                    void *y, int tokens, Epi epi, hipStream_t stream);  // trk_generic.hip
 int launch_empty(hipStream_t stream);                                  // trk_generic.hip
+int launch_empty_args(hipStream_t stream);                             // trk_generic.hip
 // elementwise consumers of fp32 outputs (trk_consume.hip)
 int launch_silu_mul(const float *g, const float *u, void *out, int out_dtype, size_t n,
                     hipStream_t stream);

@@ -116,6 +116,54 @@ struct KCfg {
                              // NW * S1 / M1T ways); 0: the default split (below)
 };
 
+// K orders of the packed second- and last-core sections a variant reads (its chain's layout):
+//   stage-2 K of (iS, r2)      = (r2 / SG) * SG * nS + iS * SG + r2 % SG
+//   stage-3 K of (iL', r1, r3) = iL' * R^2 + (r3 / LG) * LG * R + r1 * LG + r3 % LG
+// A group of R is the natural order (iS, r2) / (iL', r1, r3). Smaller groups put the four
+// results one lane stores (4 consecutive r2 or r3) next to those of the neighbouring lanes, so
+// that the stage-1 and stage-2 result stores of a half-wave fill every LDS bank once: with
+// the natural order a rank-16 16x16 tile stores its lanes 32 bytes apart (2-way bank
+// conflicts) and a 32x32 tile 32 bytes apart across its token planes (up to 4-way); measured
+// on gfx950 the conflicting stores take 2.6x as long as contiguous ones.
+constexpr int s_group(const KCfg &c) { return c.R == 8 ? 8 : 4; }
+constexpr int l_group(const KCfg &c) { return c.WIDE && c.MF2 == 32 ? 4 : 8; }
+// Bank conflicts of the stage-2 result stores: the largest number of lanes of a half-wave
+// (32 lanes, the ones one LDS pass serves for 8-byte stores) that touch one of the 64 4-byte
+// banks, for Vb planes `plane` elements apart. Lane addresses as the kernel computes them for
+// the first tile (the others add a tile constant): 32x32 tiles (w32) store rows 0..3 of
+// column lane; 16x16 tiles store rows 4 * (lane / 16) .. + 3 of column lane % 16.
+constexpr int vb_store_degree(bool w32, int Q, int R, int LG, int P3, int plane) {
+    int hits[64] = {};
+    for (int lane = 0; lane < 32; ++lane) {
+        const int m = w32 ? 0 : 4 * (lane / 16), n = w32 ? lane : lane % 16;
+        const int r3 = m % R, q = n / Q;
+        const int el = (m / R) * P3 + r3 / LG * LG * R + r3 % LG + (n % Q) * plane +
+                       q / R * R * R + q % R * LG;
+        const int bank = el * 2 / 4 % 64;
+        ++hits[bank];
+        ++hits[(bank + 1) % 64];
+    }
+    int worst = 0;
+    for (int b = 0; b < 64; ++b) worst = hits[b] > worst ? hits[b] : worst;
+    return worst;
+}
+// Pitch of the Vb planes (SC rows of one (t, f) each, `base` elements): base padded by the
+// multiple of 8 elements (rows stay 16-byte aligned) below 128 with the fewest store conflicts.
+constexpr int plane_pitch(bool w32, int Q, int R, int LG, int P3, int base) {
+    if (Q == 1) return base;
+    int best = base, worst = vb_store_degree(w32, Q, R, LG, P3, base);
+    for (int pad = 8; pad < 128 && worst > 1; pad += 8) {
+        const int d = vb_store_degree(w32, Q, R, LG, P3, base + pad);
+        if (d < worst) best = base + pad, worst = d;
+    }
+    return best;
+}
+
+// Elements of Vb: rows 0 .. M3P-1 at (row / SC) * plane + (row % SC) * P3, each P3 long.
+constexpr int vb_elems(int M3P, int SC, int P3, int plane) {
+    return (M3P - 1) / SC * plane + ((M3P - 1) % SC + 1) * P3;
+}
+
 template <KCfg C>
 struct Geo {
     static constexpr int R = C.R, R2 = R * R;
@@ -187,7 +235,14 @@ struct Geo {
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
     static constexpr int oXs = oLs + NBUF * szLs, szXs = N1P * PF;
     static constexpr int oUb = oXs + NBUF * szXs, szUb = N2R * P2;
-    static constexpr int oVb = oUb + NBUF2 * szUb, szVb = M3P * P3;
+    // Vb rows (t, f, s): planes of SC rows per (t, f), PLANE elements apart
+    static constexpr int SG = s_group(C), LG = l_group(C), Q = TT * FC;
+    // (padded to start in distinct banks where the padding fits in LDS)
+    static constexpr int oVb = oUb + NBUF2 * szUb;
+    static constexpr int PLANE_PAD = plane_pitch(W32, Q, R, LG, P3, SC * P3);
+    static constexpr int PLANE =
+        (oVb + NBUF2 * vb_elems(M3P, SC, P3, PLANE_PAD)) * 2 <= 160 * 1024 ? PLANE_PAD : SC * P3;
+    static constexpr int szVb = vb_elems(M3P, SC, P3, PLANE);
     static constexpr int LDS_ELEMS = oVb + NBUF2 * szVb;
     static constexpr int LDS_BYTES = LDS_ELEMS * 2;
     static constexpr int RED_FLOATS = (KS3 - 1) * G3 * NYW * 256;
@@ -215,6 +270,8 @@ struct Geo {
     static_assert(LDS_BYTES <= 160 * 1024, "workgroup tile exceeds the 160 KB of LDS");
     static_assert(RED_FLOATS * 4 <= szUb * 2, "stage-3 reduction does not fit in Ub");
     static_assert(nL % IC == 0, "IC must divide the last core's input mode");
+    static_assert(R % SG == 0 && R % LG == 0 && SG % 4 == 0 && LG % 4 == 0,
+                  "K-order groups must hold whole 4-element stores");
     static_assert(C.PIPE >= 0 && C.PIPE <= 2 && (C.PIPE == 0 || NSTEP > 1),
                   "a pipelined tile needs two steps");
     static_assert(XROW || IN % 8 == 0, "scatter loader reads x rows in 8-element vectors");
@@ -763,15 +820,23 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     // depends on the tile only and a part that depends on the lane only.
     //   Ub[(iL', r1, t, f)][(iS, r2)]:  stage-1 rows m = (f, r1, r2), columns n = (iL', t, iS)
     //   Vb[(t, f, s)][(iL', r1, r3)]:   stage-2 rows m = (s, r3), columns n = (iL', r1, t, f)
-    auto ub_row = [](int m) { return ((m / R) % R * G::TT * G::FC + m / R2) * G::P2 + m % R; };
+    //   (the K positions follow the chain's K orders, groups SG and LG)
+    auto ub_row = [](int m) {
+        const int r2 = m % R;
+        return ((m / R) % R * G::TT * G::FC + m / R2) * G::P2 + r2 / G::SG * G::SG * G::nS +
+               r2 % G::SG;
+    };
     auto ub_col = [](int n) {
         const int iS = n % G::nSP, t = (n / G::nSP) % G::TT, ilp = n / (G::nSP * G::TT);
-        return (ilp * R * G::TT * G::FC + t * G::FC) * G::P2 + iS * R;
+        return (ilp * R * G::TT * G::FC + t * G::FC) * G::P2 + iS * G::SG;
     };
-    auto vb_row = [](int m) { return (m / R) * G::P3 + m % R; };
-    auto vb_col = [](int n) {
-        constexpr int Q = G::FC * G::TT;  // (t, f) is n % Q, (iL', r1) is n / Q
-        return (n % Q) * G::SC * G::P3 + (n / Q) * R;
+    auto vb_row = [](int m) {
+        const int r3 = m % R;
+        return (m / R) * G::P3 + r3 / G::LG * G::LG * R + r3 % G::LG;
+    };
+    auto vb_col = [](int n) {  // (t, f) is n % Q, (iL', r1) is n / Q
+        const int q = n / G::Q;
+        return (n % G::Q) * G::PLANE + q / R * R2 + q % R * G::LG;
     };
     auto ub_tile = [&](int mt, int nt) { return ub_row(mt * 16) + ub_col(nt * 16); };
     auto vb_tile = [&](int mt, int nt) { return vb_row(mt * 16) + vb_col(nt * 16); };
@@ -873,7 +938,8 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             const int tile = g3 + G::G3 * j;
             if (G::NT3 % G::G3 == 0 || tile < G::NT3) {
                 const int mt = tile / G::N3T, nt = tile % G::N3T;
-                const E *a = vb + (mt * 16 + lrow) * G::P3;
+                const int m3 = mt * 16 + lrow;  // Vb row (t, f, s)
+                const E *a = vb + m3 / G::SC * G::PLANE + m3 % G::SC * G::P3;
                 const int l = nt * 16 + lrow;
 #pragma unroll
                 for (int q0 = 0; q0 < PERK; q0 += QB) {
@@ -1106,7 +1172,7 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
             continue;
         if (plan->nvariants == kMaxVariants) break;
         const int order[3] = {k.F, k.S, k.L};
-        const int chain = plan_chain(plan, order);
+        const int chain = plan_chain(plan, order, s_group(k), l_group(k));
         if (chain < 0) continue;
         Variant &v = plan->variants[plan->nvariants++];
         v.kind = TRK_KERNEL_MFMA;

@@ -4,8 +4,11 @@
 // values re-laid out for the kernels, zero padding only, no expansion and no dense W), own
 // layouts. For each chain (contraction order F, S, L) of the plan:
 //   Fk[f][r1][r2][KF]  = Fc[r1][f][iF][r2]   for iF < nF, else 0
-//   Sk[s][r3][K2]      = Sc[r2][s][iS][r3]   at k = iS*R + r2 < nS*R, else 0
-//   Lk[iL][l][r1][r3]  = Lc[r3][l][iL][r1]
+//   Sk[s][r3][K2]      = Sc[r2][s][iS][r3]   at k = (r2/sg)*sg*nS + iS*sg + r2%sg < nS*R,
+//                                            else 0
+//   Lk[iL][l][K]       = Lc[r3][l][iL][r1]   at K = (r3/lg)*lg*R + r1*lg + r3%lg
+// (sg = lg = R: the natural orders k = iS*R + r2, K = r1*R + r3). Only the sections a chain
+// owns are written; the others are shared with an earlier chain of the same order.
 // where a chain core Xc[in][o][i][out] is the core G[in][o][i][out] of a forward order and
 // G[out][o][i][in] of a backward one. Bits are copied, so the dtype does not matter beyond
 // its width.
@@ -23,7 +26,7 @@ __device__ inline size_t core_index(int alpha, int o, int i, int beta, int O, in
 
 struct PackArgs {
     int R, forward;
-    int nF, nS, nL, oF, oS, oL, KF, K2;
+    int nF, nS, nL, oF, oS, oL, KF, K2, sg, lg;
     size_t nFk, nSk, nLk;  // element counts of the three sections
 };
 
@@ -57,17 +60,17 @@ __global__ void __launch_bounds__(256) pack_chain_kernel(const W *__restrict__ g
             const int s = int(rest / R);
             W v = W(0);
             if (k < a.nS * R) {
-                const int iS = k / R, r2 = k % R;
+                const int span = a.sg * a.nS, rem = k % span;
+                const int iS = rem / a.sg, r2 = k / span * a.sg + rem % a.sg;
                 v = gS[a.forward ? core_index(r2, s, iS, r3, a.oS, a.nS, R)
                                  : core_index(r3, s, iS, r2, a.oS, a.nS, R)];
             }
             Sk[e] = v;
         } else {
             const size_t e = d - a.nFk - a.nSk;
-            const int r3 = int(e % R);
-            size_t rest = e / R;
-            const int r1 = int(rest % R);
-            rest /= R;
+            const int kk = int(e % (size_t(R) * R)), span = a.lg * R, rem = kk % span;
+            const int r1 = rem / a.lg, r3 = kk / span * a.lg + rem % a.lg;
+            size_t rest = e / (size_t(R) * R);
             const int l = int(rest % a.oL);
             const int iL = int(rest / a.oL);
             Lk[e] = gL[a.forward ? core_index(r3, l, iL, r1, a.oL, a.nL, R)
@@ -92,10 +95,13 @@ int pack_all(const Plan &plan, const void *const g[3], void *packed, hipStream_t
         a.oL = c.oL;
         a.KF = c.KF;
         a.K2 = c.K2;
-        a.nFk = size_t(c.oF) * c.R * c.R * c.KF;
-        a.nSk = size_t(c.oS) * c.R * c.K2;
-        a.nLk = size_t(c.nL) * c.oL * c.R * c.R;
+        a.sg = c.sg;
+        a.lg = c.lg;
+        a.nFk = c.ownF ? size_t(c.oF) * c.R * c.R * c.KF : 0;
+        a.nSk = c.ownS ? size_t(c.oS) * c.R * c.K2 : 0;
+        a.nLk = c.ownL ? size_t(c.nL) * c.oL * c.R * c.R : 0;
         const size_t total = a.nFk + a.nSk + a.nLk;
+        if (total == 0) continue;
         const int blocks = int(std::min<size_t>((total + 255) / 256, 4096));
         hipLaunchKernelGGL(pack_chain_kernel<W>, dim3(blocks), dim3(256), 0, stream,
                            static_cast<const W *>(g[c.order[0]]),

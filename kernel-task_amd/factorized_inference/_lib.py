@@ -71,6 +71,7 @@ SIGNATURES = {
                                       _c_void_p]),
     "trk_consume_add": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_size_t, _c_void_p]),
     "trk_empty_launch": (_c_int, [_c_void_p]),
+    "trk_empty_launch_args": (_c_int, [_c_void_p]),
     "trk_empty_call": (_c_int, []),
 }
 

@@ -5,7 +5,8 @@ tools/measure_kernels.py:36-103:
   stream latency   HIP events bracketing a block of back-to-back calls on the current
                    stream, divided by the block length (not a sum of kernel durations)
   host latency     wall clock around one call including the trailing synchronize
-  floors           an empty C call, and one empty kernel launch (host and stream time)
+  floors           an empty C call, and one empty kernel launch without and with the forward
+                   kernels' arguments (host and stream time)
   work             algorithmic flops of the chain order the kernel runs, and compulsory
                    bytes = element size x (factor parameters + T*in + T*out)
 """
@@ -76,12 +77,18 @@ def floors(lib, calls: int = 2000) -> dict:
         lib.trk_empty_call()
     empty_call = (time.perf_counter_ns() - t0) / 1000.0 / calls
     launch = lambda: lib.trk_empty_launch(current_stream_handle(dev))  # noqa: E731
+    # an empty kernel with the forward kernels' argument list: fetching a launch's kernel
+    # arguments is part of every forward call's stream time
+    launch_args = lambda: lib.trk_empty_launch_args(current_stream_handle(dev))  # noqa: E731
     for _ in range(50):
         launch()
+        launch_args()
     return {
         "host_empty_c_call_us": empty_call,
         "host_empty_launch_us": host_submit_us(launch, calls),
         "stream_empty_launch_us": statistics.median(stream_us(launch, 200, blocks=5)),
+        "host_empty_launch_args_us": host_submit_us(launch_args, calls),
+        "stream_empty_launch_args_us": statistics.median(stream_us(launch_args, 200, blocks=5)),
         "stream_handle": bool(stream is not None),
     }
 

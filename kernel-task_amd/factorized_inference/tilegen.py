@@ -187,6 +187,36 @@ def order_tag(order: tuple) -> str:
     return "".join(map(str, order))
 
 
+def vb_store_degree(w32: bool, q: int, R: int, lg: int, p3: int, plane: int) -> int:
+    """Worst LDS bank multiplicity of a half-wave's stage-2 result store (vb_store_degree in
+    trk_mfma_kernel.h): 32 lanes of 8-byte stores over 64 banks of 4 bytes."""
+    hits = [0] * 64
+    for lane in range(32):
+        m, n = (0, lane) if w32 else (4 * (lane // 16), lane % 16)
+        r3, qq = m % R, n // q
+        el = ((m // R) * p3 + r3 // lg * lg * R + r3 % lg + (n % q) * plane
+              + qq // R * R * R + qq % R * lg)
+        bank = el * 2 // 4 % 64
+        hits[bank] += 1
+        hits[(bank + 1) % 64] += 1
+    return max(hits)
+
+
+def plane_pitch(w32: bool, q: int, R: int, lg: int, p3: int, base: int) -> int:
+    """Pitch of the kernel's Vb planes (plane_pitch in trk_mfma_kernel.h): `base` elements plus
+    the multiple of 8 below 128 whose stores conflict least."""
+    if q == 1:
+        return base
+    best, worst = base, vb_store_degree(w32, q, R, lg, p3, base)
+    for pad in range(8, 128, 8):
+        if worst <= 1:
+            break
+        d = vb_store_degree(w32, q, R, lg, p3, base + pad)
+        if d < worst:
+            best, worst = base + pad, d
+    return best
+
+
 def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     """The kernel's compile-time geometry (struct Geo) for one tile, with the reason the
     kernel would reject it ("" when it compiles). Mirrors the static_asserts of Geo."""
@@ -233,8 +263,13 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         "Ls": nbuf * t.IC * LCP * PL,
         "Xs": nbuf * N1 * PF,
         "Ub": nbuf2 * N2R * P2,
-        "Vb": nbuf2 * M3P * P3,
     }
+    # Vb planes padded to distinct banks where the padding fits (as the kernel does)
+    vb = lambda plane: nbuf2 * ((M3P - 1) // t.SC * plane + ((M3P - 1) % t.SC + 1) * P3)  # noqa: E731
+    lg = 4 if W32 else 8  # l_group in trk_mfma_kernel.h
+    sz["Vb"] = vb(plane_pitch(W32, t.TT * t.FC, R, lg, P3, t.SC * P3))
+    if 2 * sum(sz.values()) > LDS_LIMIT:
+        sz["Vb"] = vb(t.SC * P3)
     lds = 2 * sum(sz.values())
     red_floats = (t.KS3 - 1) * G3 * NYW * 256
     k3steps = K3 // 32 if K3 % 32 == 0 else 0
