@@ -147,21 +147,54 @@ constexpr int vb_store_degree(bool w32, int Q, int R, int LG, int P3, int plane)
     for (int b = 0; b < 64; ++b) worst = hits[b] > worst ? hits[b] : worst;
     return worst;
 }
+// Bank conflicts of the stage-3 A-fragment reads of Vb (16x16x32 fragments): the largest
+// number of the first 32 lanes that read one 16-byte unit modulo 512 bytes, over every 16-row
+// tile, with rows (t, f, s) at (row / SC) * plane + (row % SC) * P3.
+constexpr int vb_read_degree(int M3T, int SC, int P3, int plane) {
+    int worst = 0;
+    for (int mt = 0; mt < M3T; ++mt) {
+        int hits[32] = {};
+        for (int lane = 0; lane < 32; ++lane) {
+            const int m3 = mt * 16 + lane % 16;
+            const int el = m3 / SC * plane + m3 % SC * P3;
+            const int u = (el / 8 + lane / 16) % 32;
+            worst = ++hits[u] > worst ? hits[u] : worst;
+        }
+    }
+    return worst;
+}
 // Pitch of the Vb planes (SC rows of one (t, f) each, `base` elements): base padded by the
-// multiple of 8 elements (rows stay 16-byte aligned) below 128 with the fewest store conflicts.
-constexpr int plane_pitch(bool w32, int Q, int R, int LG, int P3, int base) {
-    if (Q == 1) return base;
-    int best = base, worst = vb_store_degree(w32, Q, R, LG, P3, base);
-    for (int pad = 8; pad < 128 && worst > 1; pad += 8) {
-        const int d = vb_store_degree(w32, Q, R, LG, P3, base + pad);
-        if (d < worst) best = base + pad, worst = d;
+// multiple of 8 elements (rows stay 16-byte aligned) below 128 with the fewest bank conflicts
+// of the stage-2 stores and the stage-3 reads together.
+constexpr int plane_pitch(bool w32, int Q, int R, int LG, int P3, int base, int M3T, int SC) {
+    int best = base, cost = 1 << 30;
+    for (int pad = 0; pad < 128; pad += 8) {
+        const int c = vb_store_degree(w32, Q, R, LG, P3, base + pad) +
+                      vb_read_degree(M3T, SC, P3, base + pad);
+        if (c < cost) best = base + pad, cost = c;
     }
     return best;
 }
 
+// LDS row pitches (elements; K a multiple of 16). Measured on gfx950, a ds_read_b128 serves
+// 32 lanes per pass from 128 banks, so a fragment read is conflict free when those 32 lanes
+// touch 32 distinct 16-byte units modulo 512 bytes. A 32x32x16 fragment (32 rows, then the
+// same rows 16 bytes on) needs an odd pitch in 16-byte units; a 16x16x32 fragment (16 rows,
+// then the same rows 16 bytes on) needs a pitch of 2 modulo 4 units, whose 16 rows take the
+// even units and leave the odd ones to the second lane group.
+constexpr int pitch16(int K) { return K + 8 * ((6 - K / 8 % 4) % 4); }
+constexpr int pitch32(int K) { return K + 8; }
+
 // Elements of Vb: rows 0 .. M3P-1 at (row / SC) * plane + (row % SC) * P3, each P3 long.
 constexpr int vb_elems(int M3P, int SC, int P3, int plane) {
     return (M3P - 1) / SC * plane + ((M3P - 1) % SC + 1) * P3;
+}
+
+// Elements of a tile's LDS buffers for row pitches pf, p2, p3, pl (Vb planes unpadded).
+constexpr int lds_elems(bool wide, int M1, int M2P, int ls_rows, int N1P, int N2R, int M3P,
+                        int SC, int NBUF, int NBUF2, int pf, int p2, int p3, int pl) {
+    return (wide ? 16 : M1 * pf + M2P * p2) + NBUF * (ls_rows * pl + N1P * pf) +
+           NBUF2 * (N2R * p2 + vb_elems(M3P, SC, p3, SC * p3));
 }
 
 template <KCfg C>
@@ -202,12 +235,6 @@ struct Geo {
     static constexpr int NSTEP = cdiv(nL, IC);
     static constexpr int NFC = cdiv(oF, FC), NSC = cdiv(oS, SC), NLC = cdiv(oL, LC);
     static constexpr int NBLK = NFC * NSC * NLC;  // workgroups per token tile
-    // LDS row pitches: 16 bytes past the K extent (a multiple of 32 bytes), so that the 16
-    // rows one MFMA fragment read touches start in 16 distinct 16-byte bank groups
-    static constexpr int PF = KF + 8, P2 = K2 + 8, P3 = K3 + 8, PL = R2 + 8;
-    // LDS layout, in elements
-    static constexpr int oFs = 0, szFs = WIDE ? 8 : M1 * PF;
-    static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * P2;
     // WIDE: each wave holds the A fragments of BM1 stage-1 and BM2 stage-2 row tiles; stage 2
     // runs on a WM2 x WN2 grid of waves (rows x columns)
     static constexpr int WM2 = WIDE ? C.WIDE : NW, WN2 = NW / WM2;
@@ -232,6 +259,18 @@ struct Geo {
     static constexpr int TAILJ = TAIL ? (NW / 2) / TAILR : 1;
     static constexpr int NBUF = C.PIPE ? 2 : 1;  // buffers of the per-step slices
     static constexpr int NBUF2 = C.PIPE == 2 ? 2 : 1;  // buffers of the stage results
+    // LDS row pitches for the fragment shape each buffer is read with (Ub by 32x32x16 MFMAs in
+    // the W32 family, everything else by 16x16x32 or 16x16x16 MFMAs) where the tile still fits
+    // in LDS with them; otherwise 16 bytes past each K extent (conflict free for 32x32 reads)
+    static constexpr bool CFP =
+        lds_elems(WIDE, M1, M2P, IC * LCP, N1P, N2R, M3P, SC, NBUF, NBUF2, pitch16(KF),
+                  W32 ? pitch32(K2) : pitch16(K2), pitch16(K3), pitch16(R2)) * 2 <= 160 * 1024;
+    static constexpr int PF = CFP ? pitch16(KF) : KF + 8;
+    static constexpr int P2 = W32 ? pitch32(K2) : CFP ? pitch16(K2) : K2 + 8;
+    static constexpr int P3 = CFP ? pitch16(K3) : K3 + 8, PL = CFP ? pitch16(R2) : R2 + 8;
+    // LDS layout, in elements
+    static constexpr int oFs = 0, szFs = WIDE ? 8 : M1 * PF;
+    static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * P2;
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
     static constexpr int oXs = oLs + NBUF * szLs, szXs = N1P * PF;
     static constexpr int oUb = oXs + NBUF * szXs, szUb = N2R * P2;
@@ -239,7 +278,7 @@ struct Geo {
     static constexpr int SG = s_group(C), LG = l_group(C), Q = TT * FC;
     // (padded to start in distinct banks where the padding fits in LDS)
     static constexpr int oVb = oUb + NBUF2 * szUb;
-    static constexpr int PLANE_PAD = plane_pitch(W32, Q, R, LG, P3, SC * P3);
+    static constexpr int PLANE_PAD = plane_pitch(W32, Q, R, LG, P3, SC * P3, M3T, SC);
     static constexpr int PLANE =
         (oVb + NBUF2 * vb_elems(M3P, SC, P3, PLANE_PAD)) * 2 <= 160 * 1024 ? PLANE_PAD : SC * P3;
     static constexpr int szVb = vb_elems(M3P, SC, P3, PLANE);
@@ -286,9 +325,8 @@ __device__ inline void wait_loads() { __builtin_amdgcn_s_waitcnt(0); }
 // LDS <- global through VGPRs for NB blocks of BLOCK 16-byte vectors, spread over the NT
 // threads of a workgroup: block b is read from src + b * stride (vectors), its first `valid`
 // vectors from memory and the rest zero. issue() starts every read of the copy; commit(),
-// after wait_loads(), writes the LDS as rows of ROW vectors, each followed by one vector of
-// pitch padding.
-template <int NB, int BLOCK, int ROW, int NT>
+// after wait_loads(), writes the LDS as rows of ROW vectors at a pitch of PITCH vectors.
+template <int NB, int BLOCK, int ROW, int NT, int PITCH>
 struct RegCopy {
     static_assert(BLOCK % ROW == 0, "a copy block holds whole LDS rows");
     static constexpr int TOTAL = NB * BLOCK, PER = cdiv(TOTAL, NT);
@@ -307,7 +345,7 @@ struct RegCopy {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int i = threadIdx.x + j * NT;
-            if (TOTAL % NT == 0 || i < TOTAL) d[i + i / ROW] = r[j];
+            if (TOTAL % NT == 0 || i < TOTAL) d[i / ROW * PITCH + i % ROW] = r[j];
         }
     }
 };
@@ -713,9 +751,9 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             if (ilp >= 0 && ilp < G::IC) xs[((ilp * G::TT + t) * G::nSP + iS) * G::PF + iF] = e[q];
         }
     };
-    RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT> cF;
-    RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8, G::NT> cS;
-    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, G::NT> cL;
+    RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT, G::PF / 8> cF;
+    RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8, G::NT, G::P2 / 8> cS;
+    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, G::NT, G::PL / 8> cL;
     auto issue_l = [&](int iL0) TRK_INLINE {  // the last-core slice of the step at input digit iL0
         cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
     };

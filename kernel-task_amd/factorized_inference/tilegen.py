@@ -202,19 +202,42 @@ def vb_store_degree(w32: bool, q: int, R: int, lg: int, p3: int, plane: int) -> 
     return max(hits)
 
 
-def plane_pitch(w32: bool, q: int, R: int, lg: int, p3: int, base: int) -> int:
+def vb_read_degree(m3t: int, sc: int, p3: int, plane: int) -> int:
+    """Worst 16-byte-unit multiplicity of the stage-3 Vb fragment reads (vb_read_degree in
+    trk_mfma_kernel.h): the first 32 lanes of every 16-row tile, units modulo 512 bytes."""
+    worst = 0
+    for mt in range(m3t):
+        hits = [0] * 32
+        for lane in range(32):
+            m3 = mt * 16 + lane % 16
+            el = m3 // sc * plane + m3 % sc * p3
+            u = (el // 8 + lane // 16) % 32
+            hits[u] += 1
+        worst = max(worst, max(hits))
+    return worst
+
+
+def plane_pitch(w32: bool, q: int, R: int, lg: int, p3: int, base: int, m3t: int,
+                sc: int) -> int:
     """Pitch of the kernel's Vb planes (plane_pitch in trk_mfma_kernel.h): `base` elements plus
-    the multiple of 8 below 128 whose stores conflict least."""
-    if q == 1:
-        return base
-    best, worst = base, vb_store_degree(w32, q, R, lg, p3, base)
-    for pad in range(8, 128, 8):
-        if worst <= 1:
-            break
-        d = vb_store_degree(w32, q, R, lg, p3, base + pad)
-        if d < worst:
-            best, worst = base + pad, d
+    the multiple of 8 below 128 with the fewest store and stage-3 read conflicts together."""
+    best, cost = base, 1 << 30
+    for pad in range(0, 128, 8):
+        c = vb_store_degree(w32, q, R, lg, p3, base + pad) + vb_read_degree(m3t, sc, p3, base + pad)
+        if c < cost:
+            best, cost = base + pad, c
     return best
+
+
+def pitch16(k: int) -> int:
+    """LDS row pitch of a buffer read as 16x16x32 fragments (pitch16 in trk_mfma_kernel.h):
+    2 modulo 4 units of 16 bytes."""
+    return k + 8 * ((6 - k // 8 % 4) % 4)
+
+
+def pitch32(k: int) -> int:
+    """LDS row pitch of a buffer read as 32x32x16 fragments: an odd number of 16-byte units."""
+    return k + 8
 
 
 def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
@@ -246,7 +269,18 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     WM2 = t.WIDE if wide else NW
     G3 = NW // t.KS3 if t.KS3 and NW % t.KS3 == 0 else 1
     NYW = cdiv(NT3, G3)
-    PF, P2, P3, PL = KF + 8, K2 + 8, K3 + 8, R2 + 8
+    nbuf, nbuf2 = (2 if t.PIPE else 1), (2 if t.PIPE == 2 else 1)
+    N2R = cdiv(N2, 32) * 32 if W32 else N2P
+
+    def lds_elems(pf, p2, p3, pl):  # as lds_elems in trk_mfma_kernel.h (Vb planes unpadded)
+        vb = (M3P - 1) // t.SC * t.SC * p3 + ((M3P - 1) % t.SC + 1) * p3
+        return ((16 if wide else M1 * pf + M2P * p2) + nbuf * (t.IC * LCP * pl + N1 * pf)
+                + nbuf2 * (N2R * p2 + vb))
+    # pitches for the fragment shape each buffer is read with, where the tile fits with them
+    cfp = 2 * lds_elems(pitch16(KF), pitch32(K2) if W32 else pitch16(K2), pitch16(K3),
+                        pitch16(R2)) <= LDS_LIMIT
+    PF, P3, PL = (pitch16(KF), pitch16(K3), pitch16(R2)) if cfp else (KF + 8, K3 + 8, R2 + 8)
+    P2 = pitch32(K2) if W32 else pitch16(K2) if cfp else K2 + 8
     M2T32, N2T32 = cdiv(M2, 32), cdiv(N2, 32)
     if t.S1:
         BM1, WM1 = t.S1, M1T // t.S1 if M1T % t.S1 == 0 else 0
@@ -255,8 +289,6 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     else:
         BM1, WM1 = cdiv(M1T, NW), NW
     BM2 = cdiv(M2T32 if W32 else M2T, WM2)
-    N2R = N2T32 * 32 if W32 else N2P
-    nbuf, nbuf2 = (2 if t.PIPE else 1), (2 if t.PIPE == 2 else 1)
     sz = {
         "Fs": 8 if wide else M1 * PF,
         "Ss": 8 if wide else M2P * P2,
@@ -267,7 +299,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     # Vb planes padded to distinct banks where the padding fits (as the kernel does)
     vb = lambda plane: nbuf2 * ((M3P - 1) // t.SC * plane + ((M3P - 1) % t.SC + 1) * P3)  # noqa: E731
     lg = 4 if W32 else 8  # l_group in trk_mfma_kernel.h
-    sz["Vb"] = vb(plane_pitch(W32, t.TT * t.FC, R, lg, P3, t.SC * P3))
+    sz["Vb"] = vb(plane_pitch(W32, t.TT * t.FC, R, lg, P3, t.SC * P3, M3T, t.SC))
     if 2 * sum(sz.values()) > LDS_LIMIT:
         sz["Vb"] = vb(t.SC * P3)
     lds = 2 * sum(sz.values())
