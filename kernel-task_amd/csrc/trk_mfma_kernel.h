@@ -163,15 +163,23 @@ constexpr int vb_read_degree(int M3T, int SC, int P3, int plane) {
     }
     return worst;
 }
-// Pitch of the Vb planes (SC rows of one (t, f) each, `base` elements): base padded by the
-// multiple of 8 elements (rows stay 16-byte aligned) below 128 with the fewest bank conflicts
-// of the stage-2 stores and the stage-3 reads together.
-constexpr int plane_pitch(bool w32, int Q, int R, int LG, int P3, int base, int M3T, int SC) {
-    int best = base, cost = 1 << 30;
-    for (int pad = 0; pad < 128; pad += 8) {
-        const int c = vb_store_degree(w32, Q, R, LG, P3, base + pad) +
-                      vb_read_degree(M3T, SC, P3, base + pad);
-        if (c < cost) best = base + pad, cost = c;
+// Vb layout: row pitch p3 (the 16x16 pitch p3a or K3 + 8) and plane pitch SC * p3 + pad (pad a
+// multiple of 8 elements below 128, so rows stay 16-byte aligned), chosen to minimise the
+// bank conflicts of the stage-2 stores and the stage-3 reads, a conflicted store counting five
+// times a conflicted read (measured on gfx950: conflict-free 8-byte stores run at about a
+// third of the read bandwidth, and a conflicted store takes 2.6x a clean one). Returns
+// p3 * 256 + pad.
+constexpr int vb_layout(bool w32, int Q, int R, int LG, int K3, int p3a, int SC, int M3T) {
+    int best = p3a * 256, cost = 1 << 30;
+    for (int c = 0; c < 2; ++c) {
+        const int p3 = c == 0 ? p3a : K3 + 8;
+        if (c == 1 && p3 == p3a) break;
+        for (int pad = 0; pad < 128; pad += 8) {
+            const int plane = SC * p3 + pad;
+            const int k = 5 * vb_store_degree(w32, Q, R, LG, p3, plane) +
+                          vb_read_degree(M3T, SC, p3, plane);
+            if (k < cost) best = p3 * 256 + pad, cost = k;
+        }
     }
     return best;
 }
@@ -267,18 +275,19 @@ struct Geo {
                   W32 ? pitch32(K2) : pitch16(K2), pitch16(K3), pitch16(R2)) * 2 <= 160 * 1024;
     static constexpr int PF = CFP ? pitch16(KF) : KF + 8;
     static constexpr int P2 = W32 ? pitch32(K2) : CFP ? pitch16(K2) : K2 + 8;
-    static constexpr int P3 = CFP ? pitch16(K3) : K3 + 8, PL = CFP ? pitch16(R2) : R2 + 8;
+    static constexpr int PL = CFP ? pitch16(R2) : R2 + 8;
     // LDS layout, in elements
     static constexpr int oFs = 0, szFs = WIDE ? 8 : M1 * PF;
     static constexpr int oSs = oFs + szFs, szSs = WIDE ? 8 : M2P * P2;
     static constexpr int oLs = oSs + szSs, szLs = IC * LCP * PL;
     static constexpr int oXs = oLs + NBUF * szLs, szXs = N1P * PF;
     static constexpr int oUb = oXs + NBUF * szXs, szUb = N2R * P2;
-    // Vb rows (t, f, s): planes of SC rows per (t, f), PLANE elements apart
+    // Vb rows (t, f, s): planes of SC rows per (t, f), PLANE elements apart, rows P3 apart
+    // (the layout with the fewest bank conflicts, its plane padding only where it fits in LDS)
     static constexpr int SG = s_group(C), LG = l_group(C), Q = TT * FC;
-    // (padded to start in distinct banks where the padding fits in LDS)
     static constexpr int oVb = oUb + NBUF2 * szUb;
-    static constexpr int PLANE_PAD = plane_pitch(W32, Q, R, LG, P3, SC * P3, M3T, SC);
+    static constexpr int VBL = vb_layout(W32, Q, R, LG, K3, CFP ? pitch16(K3) : K3 + 8, SC, M3T);
+    static constexpr int P3 = VBL / 256, PLANE_PAD = SC * P3 + VBL % 256;
     static constexpr int PLANE =
         (oVb + NBUF2 * vb_elems(M3P, SC, P3, PLANE_PAD)) * 2 <= 160 * 1024 ? PLANE_PAD : SC * P3;
     static constexpr int szVb = vb_elems(M3P, SC, P3, PLANE);

@@ -217,15 +217,17 @@ def vb_read_degree(m3t: int, sc: int, p3: int, plane: int) -> int:
     return worst
 
 
-def plane_pitch(w32: bool, q: int, R: int, lg: int, p3: int, base: int, m3t: int,
-                sc: int) -> int:
-    """Pitch of the kernel's Vb planes (plane_pitch in trk_mfma_kernel.h): `base` elements plus
-    the multiple of 8 below 128 with the fewest store and stage-3 read conflicts together."""
-    best, cost = base, 1 << 30
-    for pad in range(0, 128, 8):
-        c = vb_store_degree(w32, q, R, lg, p3, base + pad) + vb_read_degree(m3t, sc, p3, base + pad)
-        if c < cost:
-            best, cost = base + pad, c
+def vb_layout(w32: bool, q: int, R: int, lg: int, k3: int, p3a: int, sc: int,
+              m3t: int) -> tuple[int, int]:
+    """(row pitch, plane pad) of the kernel's Vb (vb_layout in trk_mfma_kernel.h): the 16x16
+    pitch p3a or k3 + 8, and a pad below 128, minimising 5 x store + read conflicts."""
+    best, cost = (p3a, 0), 1 << 30
+    for p3 in dict.fromkeys((p3a, k3 + 8)):
+        for pad in range(0, 128, 8):
+            plane = sc * p3 + pad
+            c = 5 * vb_store_degree(w32, q, R, lg, p3, plane) + vb_read_degree(m3t, sc, p3, plane)
+            if c < cost:
+                best, cost = (p3, pad), c
     return best
 
 
@@ -279,7 +281,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     # pitches for the fragment shape each buffer is read with, where the tile fits with them
     cfp = 2 * lds_elems(pitch16(KF), pitch32(K2) if W32 else pitch16(K2), pitch16(K3),
                         pitch16(R2)) <= LDS_LIMIT
-    PF, P3, PL = (pitch16(KF), pitch16(K3), pitch16(R2)) if cfp else (KF + 8, K3 + 8, R2 + 8)
+    PF, PL = (pitch16(KF), pitch16(R2)) if cfp else (KF + 8, R2 + 8)
     P2 = pitch32(K2) if W32 else pitch16(K2) if cfp else K2 + 8
     M2T32, N2T32 = cdiv(M2, 32), cdiv(N2, 32)
     if t.S1:
@@ -296,10 +298,11 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         "Xs": nbuf * N1 * PF,
         "Ub": nbuf2 * N2R * P2,
     }
-    # Vb planes padded to distinct banks where the padding fits (as the kernel does)
-    vb = lambda plane: nbuf2 * ((M3P - 1) // t.SC * plane + ((M3P - 1) % t.SC + 1) * P3)  # noqa: E731
+    # Vb: the layout with the fewest conflicts, plane padding only where it fits (as the kernel)
     lg = 4 if W32 else 8  # l_group in trk_mfma_kernel.h
-    sz["Vb"] = vb(plane_pitch(W32, t.TT * t.FC, R, lg, P3, t.SC * P3, M3T, t.SC))
+    P3, pad = vb_layout(W32, t.TT * t.FC, R, lg, K3, pitch16(K3) if cfp else K3 + 8, t.SC, M3T)
+    vb = lambda plane: nbuf2 * ((M3P - 1) // t.SC * plane + ((M3P - 1) % t.SC + 1) * P3)  # noqa: E731
+    sz["Vb"] = vb(t.SC * P3 + pad)
     if 2 * sum(sz.values()) > LDS_LIMIT:
         sz["Vb"] = vb(t.SC * P3)
     lds = 2 * sum(sz.values())
