@@ -175,7 +175,10 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     // (stage 1 recomputed per split, the rank^3 stage divided), for token counts too small
     // to fill the GPU with variant 0's workgroups.
     Variant &g = p->variants[0];
-    g.chain = plan_chain(p, kOrders[best], p->rank, p->rank);  // natural K orders
+    // the K-order groups of the MFMA chains of the same order where the rank allows them
+    // (sections shared), the natural orders otherwise
+    const int kg = p->rank % 4 == 0 && p->rank != 8 ? 4 : p->rank;
+    g.chain = plan_chain(p, kOrders[best], kg, kg);
     const Chain &gc = p->chains[g.chain];
     int st = generic_configure(*p, g.chain, gc.oS, &g);
     if (st != TRK_OK) {

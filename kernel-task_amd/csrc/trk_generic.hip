@@ -30,6 +30,7 @@ struct GenericArgs {
     int R, RC, SG, nSG;
     int nF, nS, nL, oF, oS, oL, KF, K2;
     int sxF, sxS, sxL, syF, syS, syL;
+    int gS, gL;                                   // K-order groups of the packed Sk and Lk
     int pF, p2, pL;                               // LDS row pitches, in elements of the dtype
     int offSs, offLs, offU, offV, offY, offX;     // LDS byte offsets (Fs at 0)
 };
@@ -111,9 +112,12 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
         const int row = i / a.nF, iF = i % a.nF;
         Fs[row * a.pF + iF] = Fk[(size_t(f) * R2 + row) * a.KF + iF];
     }
+    // (Ss and Ls hold the natural K orders (iS, r2) and (r1, r3); the packed sections hold
+    // them grouped by gS and gL, as the chain's MFMA kernels read them)
     for (int i = tid; i < SGv * R * nU; i += kThreads) {
-        const int row = i / nU, k = i % nU;
-        Ss[row * a.p2 + k] = Sk[(size_t(s0) * R + row) * a.K2 + k];
+        const int row = i / nU, k = i % nU, iS = k / R, r2 = k % R;
+        const int kp = r2 / a.gS * a.gS * a.nS + iS * a.gS + r2 % a.gS;
+        Ss[row * a.p2 + k] = Sk[(size_t(s0) * R + row) * a.K2 + kp];
     }
 
     for (int t = blockIdx.y; t < a.T; t += gridDim.y) {
@@ -124,7 +128,10 @@ __global__ void __launch_bounds__(kThreads) ring3_generic_kernel(
         for (int iL = 0; iL < a.nL; ++iL) {
             __syncthreads();  // the previous iL's stage 3 is done with Ls
             const ET *lk = Lk + size_t(iL) * a.oL * R2;
-            for (int i = tid; i < a.oL * R2; i += kThreads) Ls[(i / R2) * a.pL + i % R2] = lk[i];
+            for (int i = tid; i < a.oL * R2; i += kThreads) {
+                const int l = i / R2, r1 = i % R2 / R, r3 = i % R;
+                Ls[l * a.pL + i % R2] = lk[l * R2 + r3 / a.gL * a.gL * R + r1 * a.gL + r3 % a.gL];
+            }
             for (int r1c = 0; r1c < R; r1c += RC) {
                 const int rc = min(RC, R - r1c);
                 __syncthreads();  // Ls (and Fs, Ss) written; stage 2 of the last chunk read U
@@ -243,6 +250,8 @@ int launch_generic(const Plan &plan, const Variant &v, const void *packed, const
     a.oL = c.oL;
     a.KF = c.KF;
     a.K2 = c.K2;
+    a.gS = c.sg;
+    a.gL = c.lg;
     a.sxF = c.sxF;
     a.sxS = c.sxS;
     a.sxL = c.sxL;

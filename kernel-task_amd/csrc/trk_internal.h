@@ -22,9 +22,10 @@ constexpr int kMaxChains = 12;
 //   Sk[s][r3][K2]      (k = (r2/sg)*sg*nS + iS*sg + r2%sg, zero-padded to K2)
 //                                                        second core, stage-2 operand
 //   Lk[iL][l][K]       (K = (r3/lg)*lg*R + r1*lg + r3%lg) last core, stage-3 operand
-// The K-order groups sg and lg equal R for the natural orders (iS, r2) and (r1, r3) (the
-// generic kernel) and are smaller for the MFMA kernels, whose result stores they make
-// bank-conflict free. Chains of one order share the sections whose layout agrees.
+// The K-order groups sg and lg equal R for the natural orders (iS, r2) and (r1, r3); the MFMA
+// kernels use smaller groups, which make their result stores bank-conflict free, and the
+// generic kernel reads any grouping. Chains of one order share the sections whose layout
+// agrees.
 struct Chain {
     int order[3];    // F, S, L: core indices
     int forward;     // 1 if the order follows the ring

@@ -124,9 +124,10 @@ struct KCfg {
 // that the stage-1 and stage-2 result stores of a half-wave fill every LDS bank once: with
 // the natural order a rank-16 16x16 tile stores its lanes 32 bytes apart (2-way bank
 // conflicts) and a 32x32 tile 32 bytes apart across its token planes (up to 4-way); measured
-// on gfx950 the conflicting stores take 2.6x as long as contiguous ones.
+// on gfx950 the conflicting stores take 2.6x as long as contiguous ones. At rank 8 the natural
+// orders already fill the banks for 16x16 tiles; its 32x32 tiles need a last-core group of 4.
 constexpr int s_group(const KCfg &c) { return c.R == 8 ? 8 : 4; }
-constexpr int l_group(const KCfg &c) { return c.WIDE && c.MF2 == 32 ? 4 : 8; }
+constexpr int l_group(const KCfg &c) { return c.R == 8 && !(c.WIDE && c.MF2 == 32) ? 8 : 4; }
 // Bank conflicts of the stage-2 result stores: the largest number of lanes of a half-wave
 // (32 lanes, the ones one LDS pass serves for 8-byte stores) that touch one of the 64 4-byte
 // banks, for Vb planes `plane` elements apart. Lane addresses as the kernel computes them for

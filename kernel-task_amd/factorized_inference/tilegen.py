@@ -299,7 +299,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         "Ub": nbuf2 * N2R * P2,
     }
     # Vb: the layout with the fewest conflicts, plane padding only where it fits (as the kernel)
-    lg = 4 if W32 else 8  # l_group in trk_mfma_kernel.h
+    lg = 8 if R == 8 and not W32 else 4  # l_group in trk_mfma_kernel.h
     P3, pad = vb_layout(W32, t.TT * t.FC, R, lg, K3, pitch16(K3) if cfp else K3 + 8, t.SC, M3T)
     vb = lambda plane: nbuf2 * ((M3P - 1) // t.SC * plane + ((M3P - 1) % t.SC + 1) * P3)  # noqa: E731
     sz["Vb"] = vb(t.SC * P3 + pad)
