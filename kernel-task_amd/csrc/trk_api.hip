@@ -49,22 +49,25 @@ void grid_of(const Plan &p, const Variant &v, int tokens, int grid[3]) {
 
 // Index of the chain with this order and these K-order groups in the plan, adding it (and
 // the packed sections it does not share with an earlier chain of the same order).
-int plan_chain(Plan *p, const int order[3], int sg, int lg) {
+int plan_chain(Plan *p, const int order[3], int sg, int lg, int sfrag) {
     auto same_order = [&](const Chain &c) { return std::equal(order, order + 3, c.order); };
-    for (int i = 0; i < p->nchains; ++i)
-        if (same_order(p->chains[i]) && p->chains[i].sg == sg && p->chains[i].lg == lg) return i;
+    for (int i = 0; i < p->nchains; ++i) {
+        const Chain &o = p->chains[i];
+        if (same_order(o) && o.sg == sg && o.lg == lg && o.sfrag == sfrag) return i;
+    }
     if (p->nchains == kMaxChains) return -1;
     Chain &c = p->chains[p->nchains];
     describe_chain(p->in_modes, p->out_modes, p->rank, order, &c);
     c.sg = sg;
     c.lg = lg;
+    c.sfrag = sfrag;
     c.ownF = c.ownS = c.ownL = 1;
     // sections whose layout an earlier chain of this order already has are shared
     for (int i = 0; i < p->nchains; ++i) {
         const Chain &o = p->chains[i];
         if (!same_order(o)) continue;
         if (c.ownF) { c.offF = o.offF; c.ownF = 0; }
-        if (c.ownS && o.sg == sg) { c.offS = o.offS; c.ownS = 0; }
+        if (c.ownS && o.sg == sg && o.sfrag == sfrag) { c.offS = o.offS; c.ownS = 0; }
         if (c.ownL && o.lg == lg) { c.offL = o.offL; c.ownL = 0; }
     }
     const size_t e = size_t(p->elem);
@@ -74,7 +77,7 @@ int plan_chain(Plan *p, const int order[3], int sg, int lg) {
         return off;
     };
     if (c.ownF) c.offF = take(size_t(c.oF) * c.R * c.R * c.KF);
-    if (c.ownS) c.offS = take(size_t(c.oS) * c.R * c.K2);
+    if (c.ownS) c.offS = take(size_t(sfrag ? round_up(c.oS * c.R, 32) : c.oS * c.R) * c.K2);
     if (c.ownL) c.offL = take(size_t(c.nL) * c.oL * c.R * c.R);
     return p->nchains++;
 }
@@ -178,7 +181,7 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     // the K-order groups of the MFMA chains of the same order where the rank allows them
     // (sections shared), the natural orders otherwise
     const int kg = p->rank % 4 == 0 && p->rank != 8 ? 4 : p->rank;
-    g.chain = plan_chain(p, kOrders[best], kg, kg);
+    g.chain = plan_chain(p, kOrders[best], kg, kg, 0);
     const Chain &gc = p->chains[g.chain];
     int st = generic_configure(*p, g.chain, gc.oS, &g);
     if (st != TRK_OK) {

@@ -34,6 +34,7 @@ struct Chain {
     int R;
     int KF, K2;      // padded stage-1 and stage-2 contraction lengths
     int sg, lg;      // K-order groups of the Sk and Lk sections
+    int sfrag;       // 1: Sk in 32x32x16 fragment order (trk_pack.hip)
     int sxF, sxS, sxL;  // element strides of iF, iS, iL in a row of x
     int syF, syS, syL;  // element strides of f, s, l in a row of y
     size_t offF, offS, offL;  // byte offsets of Fk, Sk, Lk in the packed buffer
@@ -84,7 +85,7 @@ int check_hip(hipError_t err, const char *what);
 void describe_chain(const int in_modes[3], const int out_modes[3], int rank, const int order[3],
                     Chain *chain);
 // index of the plan's chain with this order and K-order groups, added if new (-1: full)
-int plan_chain(Plan *plan, const int order[3], int sg, int lg);
+int plan_chain(Plan *plan, const int order[3], int sg, int lg, int sfrag);
 
 // kernels and their launchers
 int launch_pack(const Plan &plan, const void *g1, const void *g2, const void *g3, void *packed,

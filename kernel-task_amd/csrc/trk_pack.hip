@@ -7,8 +7,11 @@
 //   Sk[s][r3][K2]      = Sc[r2][s][iS][r3]   at k = (r2/sg)*sg*nS + iS*sg + r2%sg < nS*R,
 //                                            else 0
 //   Lk[iL][l][K]       = Lc[r3][l][iL][r1]   at K = (r3/lg)*lg*R + r1*lg + r3%lg
-// (sg = lg = R: the natural orders k = iS*R + r2, K = r1*R + r3). Only the sections a chain
-// owns are written; the others are shared with an earlier chain of the same order.
+// (sg = lg = R: the natural orders k = iS*R + r2, K = r1*R + r3). A chain with sfrag stores
+// Sk in the order the register-resident 32x32x16 A fragments are loaded: for each tile of 32
+// rows (s, r3) and each step of 16 k, the 64 lanes' 8-element pieces one after another
+// (lane = 32 * (k % 16 / 8) + row % 32), rows past oS*R zero. Only the sections a chain owns
+// are written; the others are shared with an earlier chain of the same order.
 // where a chain core Xc[in][o][i][out] is the core G[in][o][i][out] of a forward order and
 // G[out][o][i][in] of a backward one. Bits are copied, so the dtype does not matter beyond
 // its width.
@@ -26,7 +29,7 @@ __device__ inline size_t core_index(int alpha, int o, int i, int beta, int O, in
 
 struct PackArgs {
     int R, forward;
-    int nF, nS, nL, oF, oS, oL, KF, K2, sg, lg;
+    int nF, nS, nL, oF, oS, oL, KF, K2, sg, lg, sfrag;
     size_t nFk, nSk, nLk;  // element counts of the three sections
 };
 
@@ -54,12 +57,19 @@ __global__ void __launch_bounds__(256) pack_chain_kernel(const W *__restrict__ g
             Fk[d] = v;
         } else if (d < a.nFk + a.nSk) {
             const size_t e = d - a.nFk;
-            const int k = int(e % a.K2);
-            const size_t rest = e / a.K2;
-            const int r3 = int(rest % R);
-            const int s = int(rest / R);
+            int k, row;
+            if (a.sfrag) {  // [tile][k / 16][lane][8]
+                const int lane = int(e / 8 % 64), ks = a.K2 / 16;
+                const size_t rest = e / 512;
+                k = int(rest % ks) * 16 + lane / 32 * 8 + int(e % 8);
+                row = int(rest / ks) * 32 + lane % 32;
+            } else {
+                k = int(e % a.K2);
+                row = int(e / a.K2);
+            }
+            const int r3 = row % R, s = row / R;
             W v = W(0);
-            if (k < a.nS * R) {
+            if (k < a.nS * R && s < a.oS) {
                 const int span = a.sg * a.nS, rem = k % span;
                 const int iS = rem / a.sg, r2 = k / span * a.sg + rem % a.sg;
                 v = gS[a.forward ? core_index(r2, s, iS, r3, a.oS, a.nS, R)
@@ -97,8 +107,9 @@ int pack_all(const Plan &plan, const void *const g[3], void *packed, hipStream_t
         a.K2 = c.K2;
         a.sg = c.sg;
         a.lg = c.lg;
+        a.sfrag = c.sfrag;
         a.nFk = c.ownF ? size_t(c.oF) * c.R * c.R * c.KF : 0;
-        a.nSk = c.ownS ? size_t(c.oS) * c.R * c.K2 : 0;
+        a.nSk = c.ownS ? size_t(c.sfrag ? (c.oS * c.R + 31) / 32 * 32 : c.oS * c.R) * c.K2 : 0;
         a.nLk = c.ownL ? size_t(c.nL) * c.oL * c.R * c.R : 0;
         const size_t total = a.nFk + a.nSk + a.nLk;
         if (total == 0) continue;
