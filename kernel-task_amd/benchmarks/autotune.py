@@ -9,11 +9,16 @@ declared shape over a grid of token counts and write the fastest per token range
 
 Role of the reference's tools/qwen_sweep.py and tools/gen_v3g_tuned.py (a sweep of V3G
 tilings per Qwen shape and token count, reduced to the fastest correct tiling per token
-count, src/factorized_inference/v3g_tuned.py:4-17). Timing: HIP events around the replay of
-a HIP graph of back-to-back calls of one tile, median of three replays (GPU time per call
-without the host's per-call cost, which would hide the differences between fast tiles at
-small token counts). Every variant's
-output is checked against the shape's default variant before it may win (bitwise equality
+count, src/factorized_inference/v3g_tuned.py:4-17). Timing, median of three blocks:
+- HIP events around the replay of a HIP graph of back-to-back calls of one tile. This gives
+  the GPU time per call without the host's per-call cost (6-8 us through run_variant), which
+  would hide the differences between fast tiles;
+- for tiles that take 12 us or more, HIP events around back-to-back eager calls on the
+  stream instead, as bench.py times them. The host cost is hidden behind the kernels there,
+  and graph replays ranked some multi-stage tiles differently from eager calls (Llama up
+  T=128: a graph put two tiles 1 % apart, eager calls 7 % apart the other way).
+
+Every variant's output is checked against the shape's default variant before it may win (bitwise equality
 is not expected across tiles: the stage-3 summation order differs).
 
 Candidates span every chain order the generator searches (tilegen.search_orders); each
@@ -69,6 +74,24 @@ def graph_us(fn, calls: int, blocks: int = 3) -> float:
     return statistics.median(out)
 
 
+def eager_us(fn, calls: int, blocks: int = 3) -> float:
+    """Stream time per call of `calls` back-to-back eager calls, median of `blocks` blocks."""
+    out = []
+    for _ in range(blocks):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(calls):
+            fn()
+        e.record()
+        e.synchronize()
+        out.append(s.elapsed_time(e) * 1000.0 / calls)
+    return statistics.median(out)
+
+
+EAGER_FROM_US = 12.0  # tiles this slow (graph-timed) are re-timed with eager calls
+
+
 def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
     dtype = torch.bfloat16 if shape.dtype == "bf16" else torch.float16
     spec = TRSpec(shape.ins, shape.outs, shape.rank)
@@ -105,7 +128,12 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
             torch.cuda.synchronize()
             one = (time.perf_counter() - t0) * 1e6
             calls = max(5, min(50, int(2e3 / max(one, 1.0))))
-            row[names[i]] = graph_us(fn, calls)
+            us = graph_us(fn, calls)
+            if us >= EAGER_FROM_US:
+                for _ in range(calls):  # the clock settles under load first
+                    fn()
+                us = eager_us(fn, calls)
+            row[names[i]] = us
         measured[T] = row
         best = min(row, key=row.get)
         print(f"{shape.key} T={T:4d}: " + "  ".join(
