@@ -232,6 +232,8 @@ def test_every_variant(shape, rank, dtype):
     ((2, 3, 2), (2, 4, 3), 2), ((4, 4, 4), (4, 4, 4), 8), ((4, 4, 4), (4, 4, 4), 16),
     ((3, 2, 5), (4, 3, 6), 3), ((5, 7, 3), (3, 5, 7), 5), ((1, 1, 1), (1, 1, 1), 1),
     ((8, 12, 20), (12, 10, 24), 4),
+    ((4, 4, 4), (4, 4, 4), 12),  # generic kernel on K orders grouped by 4 at a rank that is
+                                 # not a power of two
 ])
 def test_odd_shapes(ins, outs, rank, dtype):
     announce(test="odd", ins=ins, outs=outs, rank=rank, dtype=dtype)
