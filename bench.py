@@ -13,7 +13,10 @@ synchronizes, with x and the packed cores resident in HBM.
 The same line carries the other metric cases (tokens 8/32 at rank 8, 1/32 at rank 16, and
 the bf16 Llama-shaped configs) with the dense GEMM of the same shape (F.linear on the
 materialised weight, timed the same way), the dominant kernel's roofline, the launch floors
-and the CPU baseline (the oracle's port of the reference path, fp32, timed on this host).
+and the CPU baseline (the oracle's port of the reference path and the package's torch
+restatement of it, fp32, timed on this host). Every case is checked against the fp32
+factorized path after timing; a result outside the acceptance tolerance ends the run with a
+non-zero status and no JSON line.
 """
 from __future__ import annotations
 
@@ -30,7 +33,12 @@ ROOT = Path(__file__).resolve().parent
 # memory and reads them back before each launch, which costs ~1.5 us of host time per launch
 # with arguments (every launch measured here, ours and the dense GEMM alike). Set before HIP
 # initialises; an explicit setting in the environment wins.
-os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "0")
+# `--runtime-default-child` is the child process that times the headline under the runtime's
+# own default (the setting unset), reported next to the tuned figure.
+if "--runtime-default-child" in sys.argv[1:]:
+    os.environ.pop("HIP_FORCE_DEV_KERNARG", None)
+else:
+    os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "0")
 sys.path.insert(0, str(ROOT / "kernel-task_amd"))
 sys.path.insert(0, str(ROOT))
 
@@ -49,7 +57,14 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup, headline):
+# Acceptance per case (tests/test_correctness.py:17-23 and BASELINE.json north_star): the
+# elementwise rule |y - y_ref| <= tol + tol*|y_ref| and, for 16-bit types,
+# max|y - y_ref| <= 1e-2 * max|y_ref|.
+TOLERANCE = {"float16": 2e-2, "bfloat16": 2e-2, "float32": 1e-4}
+
+
+def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup, headline,
+                 profile_kernels=True):
     import torch
 
     from factorized_inference import (TRSpec, dense_forward, make_cores,
@@ -108,11 +123,26 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
         y = run(x)
         m.synchronize()
         call_extra = torch.cuda.max_memory_allocated() - torch.cuda.memory_allocated()
+        # kernel-only device time per dispatch (torch.profiler over 20 back-to-back calls,
+        # the reference's tools/measure_kernels.py:69-82 protocol)
+        kernel = None
+        if profile_kernels:
+            times = m.kernel_us(ours, 20)
+            ring = {k: v for k, v in times.items() if "ring3" in k}
+            if ring:
+                name, kernel = max(ring.items(), key=lambda kv: kv[1]["dispatches"])
         # correctness after timing, against the fp32 factorized path on the same cores
         y = y.float()
         ref = tr_forward_reference(x.float(), [c.float() for c in cores], spec)
-        err = (y - ref).abs().max().item()
+        diff = (y - ref).abs()
+        err = diff.max().item()
+        tol = TOLERANCE[dtype_name]
+        ok = bool((diff <= tol + tol * ref.abs()).all().item()) and bool(torch.isfinite(y).all())
+        if dtype_name != "float32":
+            ok = ok and err <= 1e-2 * ref.abs().max().item()
         info = run.selected(T)
+        ref_flops = m.reference_flops(spec, T)
+        peak = m.PEAK_TFLOPS[dtype]
         case = {
             "case": label, "tokens": T, "rank": rank, "dtype": dtype_name,
             "modes": [list(ins), list(outs)], "variant": info["name"], "grid": info["grid"],
@@ -126,61 +156,103 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
             "prepare_held_bytes": prep_held, "prepare_peak_bytes": prep_peak,
             "call_extra_bytes": call_extra,
             "dense_weight_bytes": weight.numel() * weight.element_size(),
+            "passed": ok,
             **m.roofline(info["flops"], info["bytes"], ours_us, dtype),
+            # the reference's flop count (its fixed order) at the same time, for comparison
+            # with its "% FP16 TC peak" column
+            "reference_flops": ref_flops,
+            "frac_mfma_reference_flops": ref_flops / (ours_us * 1e-6) / 1e12 / peak,
         }
+        if kernel is not None:
+            case.update({
+                "kernel_us": kernel["avg_us"], "kernel_min_us": kernel["min_us"],
+                "kernel_frac_hbm": info["bytes"] / (kernel["avg_us"] * 1e-6) / 1e9 / m.PEAK_HBM_GBS,
+                "kernel_frac_mfma": info["flops"] / (kernel["avg_us"] * 1e-6) / 1e12 / peak,
+                "kernel_frac_mfma_reference_flops":
+                    ref_flops / (kernel["avg_us"] * 1e-6) / 1e12 / peak,
+            })
         log(f"{label} T={T}: ours {ours_us:.2f} us, dense {dense_us:.2f} us, "
-            f"err {err:.2e}, {info['name']}")
+            f"kernel {kernel['avg_us'] if kernel else float('nan'):.2f} us, "
+            f"err {err:.2e}{'' if ok else ' FAILED'}, {info['name']}")
         results.append(case)
     return results
 
 
 def cpu_baseline(seconds: float) -> dict:
-    """The oracle's port of the reference CPU path (fp32, reference order), config 1."""
+    """The reference CPU path, config 1 (1920->2880, R8, fp32, T=1, per-core sigma, seed 0),
+    timed on this host: the oracle's numpy port of the reference's three contractions
+    (`value`, 1 BLAS thread, about `seconds` of work) and, beside it, the package's torch
+    restatement of tr_forward_reference (the reference's own CPU path: permute + matmul
+    through torch's CPU BLAS) at 1 thread and at every thread count up to the host's."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
 
-    from factorized_inference import TRSpec, make_cores
+    from factorized_inference import TRSpec, make_cores, tr_forward_reference
     from oracle import ring_oracle
 
     spec = TRSpec()
-    cores = [c.numpy() for c in make_cores(spec, seed=0)]
-    x = torch.randn(1, spec.in_features, generator=torch.Generator().manual_seed(1)).numpy()
-    out = {}
-    for threads in (1, os.cpu_count() or 1):
-        with threadpool_limits(limits=threads):
-            for _ in range(20):
-                ring_oracle.tr_forward(x, cores)
-            samples = []
-            budget = seconds if threads == 1 else seconds / 3
-            t_end = time.perf_counter() + budget
-            while time.perf_counter() < t_end or len(samples) < 100:
-                t0 = time.perf_counter_ns()
-                y = ring_oracle.tr_forward(x, cores)
-                samples.append((time.perf_counter_ns() - t0) / 1000.0)
-        out[threads] = (statistics.median(samples), len(samples))
-        assert np.isfinite(y).all()
-    one, n1 = out[1]
-    many, nmany = out[max(out)]
+    cores_t = make_cores(spec, seed=0)
+    cores = [c.numpy() for c in cores_t]
+    x_t = torch.randn(1, spec.in_features, generator=torch.Generator().manual_seed(1))
+    x = x_t.numpy()
+
+    def sample(fn, budget):
+        for _ in range(20):
+            fn()
+        samples = []
+        t_end = time.perf_counter() + budget
+        while time.perf_counter() < t_end or len(samples) < 100:
+            t0 = time.perf_counter_ns()
+            fn()
+            samples.append((time.perf_counter_ns() - t0) / 1000.0)
+        return statistics.median(samples), len(samples)
+
+    with threadpool_limits(limits=1):
+        port_us, port_n = sample(lambda: ring_oracle.tr_forward(x, cores), seconds)
+        assert np.isfinite(ring_oracle.tr_forward(x, cores)).all()
+    host = os.cpu_count() or 1
+    counts = sorted({1, 2, 4, 8, 16, host} & set(range(1, host + 1)))
+    before = torch.get_num_threads()
+    torch_path = {}
+    try:
+        with torch.inference_mode():
+            for n in counts:
+                torch.set_num_threads(n)
+                us, calls = sample(lambda: tr_forward_reference(x_t, cores_t, spec),
+                                   seconds / 2 if n == 1 else seconds / 8)
+                torch_path[str(n)] = {"us": us, "calls": calls}
+    finally:
+        torch.set_num_threads(before)
+    # the baseline is the fastest CPU figure measured (the torch path at its best thread
+    # count); the oracle port and every thread count are kept beside it
+    best_threads, best = min(torch_path.items(), key=lambda kv: kv[1]["us"])
     return {
-        "value": one, "unit": "us/call", "cores": 1, "kind": "port",
+        "value": best["us"], "unit": "us/call", "cores": int(best_threads), "kind": "port",
         "sample": (f"config 1 (1920->2880, R8, fp32, T=1, per-core sigma, seed 0): median of "
-                   f"{n1} calls of oracle/ring_oracle.tr_forward (the reference's three "
-                   f"contractions in its order, numpy BLAS) with 1 BLAS thread"),
-        "all_cores_value": many, "all_cores": max(out), "all_cores_calls": nmany,
-        "cpu_model": _cpu_model(),
+                   f"{best['calls']} calls of tr_forward_reference on the CPU (the reference's "
+                   f"three contractions in its order, torch CPU BLAS, {best_threads} threads)"),
+        "torch_reference_path_us": torch_path,
+        "oracle_port_us": port_us, "oracle_port_calls": port_n, "oracle_port_threads": 1,
+        "host_threads": host, "cpu_model": _cpu_model(),
     }
 
 
 def _cpu_model() -> str:
+    """The host CPU's model name, family and model numbers (/proc/cpuinfo)."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, value = line.partition(":")
+                key = key.strip()
+                if key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                    fields[key] = value.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    return (f"{name} (family {fields.get('cpu family', '?')}, model {fields.get('model', '?')}, "
+            f"stepping {fields.get('stepping', '?')})")
 
 
 def traffic_probe(calls: int) -> None:
@@ -208,14 +280,72 @@ def traffic_probe(calls: int) -> None:
           f"{src.numel() * 2} bytes", flush=True)
 
 
+def runtime_default_child(steps: int, warmup: int) -> int:
+    """Child process: the headline measured exactly as in the parent, under the HIP
+    runtime's default kernel-argument placement (HIP_FORCE_DEV_KERNARG unset)."""
+    import torch
+
+    from factorized_inference import measure as m
+
+    torch.set_num_threads(1)
+    with torch.inference_mode():
+        a = torch.randn(4096, 4096, device="cuda", dtype=torch.float16)
+        t_end = time.perf_counter() + 0.5
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                a @ a
+            torch.cuda.synchronize()
+        del a
+        label, ins, outs, rank, dt, init, _ = CASES[0]
+        case = measure_case(label, ins, outs, rank, dt, init, (1,), steps, warmup,
+                            headline=True, profile_kernels=False)[0]
+        from factorized_inference import TRSpec, make_cores, prepare_optimized
+
+        spec = TRSpec(ins, outs, rank)
+        run = prepare_optimized(make_cores(spec, device="cuda", dtype=torch.float16, seed=0), spec)
+        x = torch.randn(1, spec.in_features, generator=torch.Generator(device="cuda").manual_seed(1),
+                        device="cuda", dtype=torch.float16)
+        blocks = m.stream_us(lambda: run(x), steps, blocks=9)
+    print(json.dumps({"value": case["ours_stream_us"], "median_of_9_blocks": statistics.median(blocks),
+                      "submit_us": case["ours_submit_us"], "passed": case["passed"],
+                      "hip_force_dev_kernarg": os.environ.get("HIP_FORCE_DEV_KERNARG")}), flush=True)
+    return 0 if case["passed"] else 1
+
+
+def runtime_default_figure(steps: int, warmup: int) -> dict | None:
+    """Runs runtime_default_child in a fresh process (the setting is read once, when HIP
+    initialises) and returns what it printed, or None if it failed."""
+    import subprocess
+
+    env = {k: v for k, v in os.environ.items() if k != "HIP_FORCE_DEV_KERNARG"}
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--runtime-default-child",
+           "--steps", str(steps), "--warmup", str(warmup)]
+    try:
+        done = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        log("runtime-default child timed out")
+        return None
+    if done.returncode != 0:
+        log(f"runtime-default child failed ({done.returncode}): {done.stderr[-2000:]}")
+        return None
+    return json.loads(done.stdout.strip().splitlines()[-1])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--no-kernel-profiler", action="store_true",
+                    help="skip the in-process torch.profiler kernel times (for runs under "
+                         "rocprofv3, which traces the same dispatches itself)")
+    ap.add_argument("--no-runtime-default", action="store_true",
+                    help="skip the child process that times the headline under the runtime's "
+                         "default kernel-argument placement")
+    ap.add_argument("--runtime-default-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="CALLS",
                     help="only run the workload of the HBM-traffic counter runs")
     args = ap.parse_args()
@@ -226,6 +356,8 @@ def main() -> int:
     if args.traffic_probe:
         traffic_probe(args.traffic_probe)
         return 0
+    if args.runtime_default_child:
+        return runtime_default_child(args.steps, args.warmup)
 
     import torch
 
@@ -238,6 +370,7 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
     torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
     torch.set_num_threads(1)
+    profile = not args.no_kernel_profiler
     with torch.inference_mode():
         # bring the GPU to its working clock before the first case (dense GEMMs, untimed)
         a = torch.randn(4096, 4096, device="cuda", dtype=torch.float16)
@@ -252,14 +385,32 @@ def main() -> int:
             if args.headline_only and i > 0:
                 break
             cases += measure_case(label, ins, outs, rank, dt, init, tokens, args.steps,
-                                  args.warmup, headline=(i == 0))
-        floors = m.floors(_lib.load())
+                                  args.warmup, headline=(i == 0), profile_kernels=profile)
+        floors = m.floors(_lib.load(), profiler=profile)
+    failed = [f"{c['case']} T={c['tokens']}" for c in cases if not c["passed"]]
+    if failed:
+        log(f"results outside the acceptance tolerance: {', '.join(failed)}; no bench line")
+        return 1
     head = cases[0]
+    default_runtime = None if args.no_runtime_default else runtime_default_figure(
+        args.steps, args.warmup)
     traffic = None
     traffic_file = ROOT / "profiles" / "traffic_r8_t1.json"
     if traffic_file.exists():
         traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
     achieved = head["achieved_GBps"]
+    roof = {"bound": "hbm", "achieved": achieved, "peak": m.PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": achieved / m.PEAK_HBM_GBS, "traffic": traffic,
+            "kernel": head["variant"], "algorithmic_bytes": head["bytes"],
+            "time_us": head["ours_stream_us"], "time_source": "HIP events over the timed block",
+            "mfma_frac": head["frac_mfma"],
+            "mfma_frac_reference_flops": head["frac_mfma_reference_flops"],
+            "floor_stream_empty_args_us": floors["stream_empty_launch_args_us"],
+            "floor_stream_empty_us": floors["stream_empty_launch_us"]}
+    if "kernel_us" in head:
+        roof.update({"kernel_us": head["kernel_us"], "kernel_frac": head["kernel_frac_hbm"],
+                     "kernel_time_source": "torch.profiler kernel events, 20 back-to-back calls",
+                     "floor_kernel_empty_args_us": floors.get("kernel_empty_args_us")})
     line = {
         "metric": METRIC,
         "value": head["ours_stream_us"],
@@ -277,12 +428,10 @@ def main() -> int:
         "config": {"workload": "tensor-ring linear 1920->2880, modes (8,12,20)->(12,10,24), "
                                "rank 8, fp16, tokens 1 (BASELINE configs[1])",
                    "tokens": 1, "rank": 8, "in_features": 1920, "out_features": 2880,
-                   "hip_force_dev_kernarg": os.environ.get("HIP_FORCE_DEV_KERNARG")},
+                   "hip_force_dev_kernarg": os.environ.get("HIP_FORCE_DEV_KERNARG"),
+                   "runtime_default": default_runtime},
         "dense_stream_us": head["dense_stream_us"],
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": m.PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": achieved / m.PEAK_HBM_GBS, "traffic": traffic,
-                     "kernel": head["variant"], "algorithmic_bytes": head["bytes"],
-                     "mfma_frac": head["frac_mfma"]},
+        "roofline": roof,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
         "floors": floors,
         "cases": cases,

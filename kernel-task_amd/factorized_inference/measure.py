@@ -5,10 +5,15 @@ tools/measure_kernels.py:36-103:
   stream latency   HIP events bracketing a block of back-to-back calls on the current
                    stream, divided by the block length (not a sum of kernel durations)
   host latency     wall clock around one call including the trailing synchronize
+  kernel time      device time per dispatch from torch.profiler kernel events over a block
+                   of back-to-back calls (tools/measure_kernels.py:69-82); on ROCm its
+                   timestamps bracket the dispatch as the tracer sees it, so a short kernel
+                   reads longer than its share of the stream period
   floors           an empty C call, and one empty kernel launch without and with the forward
-                   kernels' arguments (host and stream time)
-  work             algorithmic flops of the chain order the kernel runs, and compulsory
-                   bytes = element size x (factor parameters + T*in + T*out)
+                   kernels' arguments (host and stream time, and profiler kernel time)
+  work             algorithmic flops of the chain order the kernel runs, the reference's
+                   flop count (its fixed order, tools/measure_kernels.py:36-44), and
+                   compulsory bytes = element size x (factor parameters + T*in + T*out)
 """
 from __future__ import annotations
 
@@ -66,8 +71,41 @@ def host_submit_us(fn: Callable[[], object], calls: int) -> float:
     return (t1 - t0) / 1000.0 / calls
 
 
-def floors(lib, calls: int = 2000) -> dict:
-    """Host cost of an empty C call and of an empty launch; stream time of empty launches."""
+def kernel_us(fn: Callable[[], object], calls: int = 20) -> dict[str, dict]:
+    """Per kernel name: dispatches and average / minimum device time per dispatch (us) from
+    torch.profiler's kernel events over `calls` back-to-back calls after 3 warm-up calls."""
+    from torch.autograd import DeviceType
+    from torch.profiler import ProfilerActivity, profile
+
+    for _ in range(3):
+        fn()
+    synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        for _ in range(calls):
+            fn()
+        synchronize()
+    per: dict[str, list[float]] = {}
+    for ev in prof.events():
+        if ev.device_type == DeviceType.CUDA:
+            per.setdefault(ev.name, []).append(ev.time_range.elapsed_us())
+    return {name: {"dispatches": len(v), "avg_us": sum(v) / len(v), "min_us": min(v)}
+            for name, v in per.items()}
+
+
+def reference_flops(spec, tokens: int) -> float:
+    """Flops of the reference's fixed contraction order (G1, G2, G3) for `tokens` tokens
+    (tools/measure_kernels.py:36-44): the count its "% FP16 TC peak" column uses."""
+    ni, nj, nk = spec.input_modes
+    P, Q, Rr = spec.output_modes
+    R = spec.rank
+    per_token = ni * nj * nk * P * R * R + nj * nk * P * Q * R ** 3 + nk * P * Q * Rr * R * R
+    return 2.0 * tokens * per_token
+
+
+def floors(lib, calls: int = 2000, profiler: bool = True) -> dict:
+    """Host cost of an empty C call and of an empty launch; stream time of empty launches;
+    with `profiler`, the profiler's kernel time of the empty kernels (the reference's
+    kernel_empty_us, tools/measure_kernels.py:97-103)."""
     from .tr_kernel import current_stream_handle
 
     dev = torch.cuda.current_device()
@@ -83,7 +121,7 @@ def floors(lib, calls: int = 2000) -> dict:
     for _ in range(50):
         launch()
         launch_args()
-    return {
+    out = {
         "host_empty_c_call_us": empty_call,
         "host_empty_launch_us": host_submit_us(launch, calls),
         "stream_empty_launch_us": statistics.median(stream_us(launch, 200, blocks=5)),
@@ -91,6 +129,12 @@ def floors(lib, calls: int = 2000) -> dict:
         "stream_empty_launch_args_us": statistics.median(stream_us(launch_args, 200, blocks=5)),
         "stream_handle": bool(stream is not None),
     }
+    if profiler:
+        for key, fn in (("kernel_empty_us", launch), ("kernel_empty_args_us", launch_args)):
+            times = kernel_us(fn)
+            out[key] = sum(t["avg_us"] * t["dispatches"] for t in times.values()) / max(
+                1, sum(t["dispatches"] for t in times.values()))
+    return out
 
 
 def roofline(flops: float, nbytes: float, us: float, dtype: torch.dtype) -> dict:

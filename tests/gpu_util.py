@@ -13,16 +13,20 @@ TOLERANCE = {torch.float16: 2e-2, torch.bfloat16: 2e-2, torch.float32: 1e-4}
 MAX_ABS_FRACTION = 1e-2
 
 
-def oracle_y(x: torch.Tensor, cores, spec) -> np.ndarray:
+def oracle_y(x: torch.Tensor, cores, spec, chunk: int = 0) -> np.ndarray:
     """float64 oracle output for the exact (already rounded) x and cores, on the CPU.
 
     Contracts in the cheapest order; every order equals the reference's to ~1e-14
-    (tests/test_oracle.py)."""
+    (tests/test_oracle.py). chunk > 0 runs `chunk` token rows at a time (token rows are
+    independent), which bounds the float64 intermediates at large token counts."""
     xs = x.detach().double().cpu().numpy()
     cs = [c.detach().double().cpu().numpy() for c in cores]
     order = min(orc.CHAIN_ORDERS,
                 key=lambda o: orc.flops_per_token(spec.input_modes, spec.output_modes, spec.rank, o))
-    return orc.chain_forward(xs, cs, order)
+    if chunk <= 0 or xs.shape[0] <= chunk:
+        return orc.chain_forward(xs, cs, order)
+    return np.concatenate([orc.chain_forward(xs[t:t + chunk], cs, order)
+                           for t in range(0, xs.shape[0], chunk)])
 
 
 def check_result(actual: torch.Tensor, expected: np.ndarray, dtype: torch.dtype) -> dict:
