@@ -4,6 +4,8 @@ declared shape over a grid of token counts and write the fastest per token range
     python -m factorized_inference.tilegen --all   # compile every candidate (from kernel-task_amd/)
     python -m factorized_inference.build_ext
     python kernel-task_amd/benchmarks/autotune.py --out gpurun_out/tuned.json    # on an MI355X
+        (the winners' table; the raw timings of every candidate go to --measurements,
+        gpurun_out/autotune_us.json by default, and never into the tree)
     cp gpurun_out/tuned.json kernel-task_amd/csrc/gen/tuned.json
     python -m factorized_inference.tilegen && python -m factorized_inference.build_ext
 
@@ -92,7 +94,7 @@ def eager_us(fn, calls: int, blocks: int = 3) -> float:
 EAGER_FROM_US = 12.0  # tiles this slow (graph-timed) are re-timed with eager calls
 
 
-def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
+def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
     dtype = torch.bfloat16 if shape.dtype == "bf16" else torch.float16
     spec = TRSpec(shape.ins, shape.outs, shape.rank)
     cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init="uniform")
@@ -159,8 +161,8 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> dict:
     for r in ranges:
         r["order"] = list(tiles[r["name"]][0])
         r["tile"] = asdict(tiles[r["name"]][1])
-    return {"order": list(order), "device": torch.cuda.get_device_name(0),
-            "measured_us": {str(T): row for T, row in measured.items()}, "ranges": ranges}
+    return ({"order": list(order), "device": torch.cuda.get_device_name(0), "ranges": ranges},
+            {str(T): row for T, row in measured.items()})
 
 
 def main() -> int:
@@ -168,12 +170,15 @@ def main() -> int:
     ap.add_argument("--out", type=Path, required=True)
     ap.add_argument("--shapes", default="", help="comma-separated shape keys (default: all)")
     ap.add_argument("--seconds-per-shape", type=float, default=60.0)
+    ap.add_argument("--measurements", type=Path, default=Path("gpurun_out/autotune_us.json"),
+                    help="where the raw per-candidate timings go (not part of the tables)")
     args = ap.parse_args()
     if not torch.cuda.is_available():
         print("autotune.py needs a ROCm GPU", file=sys.stderr)
         return 1
     wanted = set(filter(None, args.shapes.split(",")))
     result = json.loads(args.out.read_text()) if args.out.exists() else {}
+    raw = json.loads(args.measurements.read_text()) if args.measurements.exists() else {}
     with torch.inference_mode():
         # bring the GPU to its working clock first (the first timings would read slow)
         a = torch.randn(4096, 4096, device="cuda", dtype=torch.float16)
@@ -186,9 +191,10 @@ def main() -> int:
         for shape in tilegen.DECLARED:
             if wanted and shape.key not in wanted:
                 continue
-            result[shape.key] = tune_shape(shape, args.seconds_per_shape)
-            args.out.parent.mkdir(parents=True, exist_ok=True)
-            args.out.write_text(json.dumps(result, indent=1, sort_keys=True) + "\n")
+            result[shape.key], raw[shape.key] = tune_shape(shape, args.seconds_per_shape)
+            for path, data in ((args.out, result), (args.measurements, raw)):
+                path.parent.mkdir(parents=True, exist_ok=True)
+                path.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
     print(f"wrote {args.out}", flush=True)
     return 0
 

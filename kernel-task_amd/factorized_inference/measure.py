@@ -48,14 +48,16 @@ def stream_us(fn: Callable[[], object], calls: int, blocks: int = 1) -> list[flo
     return out
 
 
-def host_us(fn: Callable[[], object], samples: int) -> list[float]:
-    """Host-synchronized latency (us) of single calls."""
+def host_us(fn: Callable[[], object], samples: int,
+            sync: Callable[[], None] = synchronize) -> list[float]:
+    """Host-synchronized latency (us) of single calls (`sync` waits for the device; a no-op
+    for work on the CPU)."""
     out = []
     for _ in range(samples):
-        synchronize()
+        sync()
         t0 = time.perf_counter_ns()
         fn()
-        synchronize()
+        sync()
         out.append((time.perf_counter_ns() - t0) / 1000.0)
     return out
 
