@@ -50,6 +50,17 @@ using f32x4 = float __attribute__((ext_vector_type(4)));
 #define TRK_INLINE __attribute__((always_inline))
 using f32x16 = float __attribute__((ext_vector_type(16)));
 
+// Accumulator of a 16x16xK MFMA chain. Each MFMA of Ops takes and returns the accumulator
+// type of its own K, so a chain that mixes 16x16x32 and 16x16x16 MFMAs on one accumulator
+// does not compile: such a mixed chain gave wrong sums on gfx950 in one schedule (the first two
+// of every four accumulator elements short of their last contributions). A K that ends in 16
+// after 32-wide steps therefore finishes with one more 16x16x32 MFMA whose upper K half is
+// zero; 16x16x16 MFMAs only serve a K of 16 alone, on an Acc<16> of their own.
+template <int K>
+struct Acc {
+    f32x4 v;
+};
+
 template <int DT>
 struct Ops;
 
@@ -59,11 +70,11 @@ struct Ops<TRK_DTYPE_F16> {
     using V8 = _Float16 __attribute__((ext_vector_type(8)));
     using V4 = _Float16 __attribute__((ext_vector_type(4)));
     using E4 = V4;
-    __device__ static f32x4 k32(V8 a, V8 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    __device__ static Acc<32> k32(V8 a, V8 b, Acc<32> c) {
+        return {__builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c.v, 0, 0, 0)};
     }
-    __device__ static f32x4 k16(V4 a, V4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    __device__ static Acc<16> k16(V4 a, V4 b, Acc<16> c) {
+        return {__builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c.v, 0, 0, 0)};
     }
     __device__ static f32x16 w16(V8 a, V8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -76,11 +87,11 @@ struct Ops<TRK_DTYPE_BF16> {
     using V8 = __bf16 __attribute__((ext_vector_type(8)));
     using V4 = short __attribute__((ext_vector_type(4)));  // the K16 bf16 MFMA takes raw bits
     using E4 = __bf16 __attribute__((ext_vector_type(4)));
-    __device__ static f32x4 k32(V8 a, V8 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    __device__ static Acc<32> k32(V8 a, V8 b, Acc<32> c) {
+        return {__builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c.v, 0, 0, 0)};
     }
-    __device__ static f32x4 k16(V4 a, V4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    __device__ static Acc<16> k16(V4 a, V4 b, Acc<16> c) {
+        return {__builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c.v, 0, 0, 0)};
     }
     __device__ static f32x16 w16(V8 a, V8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -422,28 +433,30 @@ __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename 
         const int m0 = (blk / NBN) * BM, n0 = (blk % NBN) * BN;
         const typename O::E *a = A + (m0 * 16 + lrow) * P;
         const typename O::E *b = B + (n0 * 16 + lrow) * P;
-        f32x4 d[BM][BN];
+        Acc<(K32 > 0 ? 32 : 16)> d[BM][BN];
 #pragma unroll
         for (int i = 0; i < BM; ++i)
 #pragma unroll
-            for (int q = 0; q < BN; ++q) d[i][q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int q = 0; q < BN; ++q) d[i][q].v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (K32 > 0) {
 #pragma unroll
-        for (int k = 0; k < K32; ++k) {
-            V8 af[BM], bf[BN];
+            for (int k = 0; k < K32; ++k) {
+                V8 af[BM], bf[BN];
 #pragma unroll
-            for (int i = 0; i < BM; ++i)
-                af[i] = (MT % BM == 0 || m0 + i < MT)
-                            ? *reinterpret_cast<const V8 *>(a + i * 16 * P + 32 * k + 8 * lgrp)
-                            : V8{};
+                for (int i = 0; i < BM; ++i)
+                    af[i] = (MT % BM == 0 || m0 + i < MT)
+                                ? *reinterpret_cast<const V8 *>(a + i * 16 * P + 32 * k + 8 * lgrp)
+                                : V8{};
 #pragma unroll
-            for (int q = 0; q < BN; ++q)
-                bf[q] = (NT % BN == 0 || n0 + q < NT)
-                            ? *reinterpret_cast<const V8 *>(b + q * 16 * P + 32 * k + 8 * lgrp)
-                            : V8{};
+                for (int q = 0; q < BN; ++q)
+                    bf[q] = (NT % BN == 0 || n0 + q < NT)
+                                ? *reinterpret_cast<const V8 *>(b + q * 16 * P + 32 * k + 8 * lgrp)
+                                : V8{};
 #pragma unroll
-            for (int i = 0; i < BM; ++i)
+                for (int i = 0; i < BM; ++i)
 #pragma unroll
-                for (int q = 0; q < BN; ++q) d[i][q] = O::k32(af[i], bf[q], d[i][q]);
+                    for (int q = 0; q < BN; ++q) d[i][q] = O::k32(af[i], bf[q], d[i][q]);
+            }
         }
         if constexpr (K16 && K32 > 0) {
             // trailing 16 of K after 32-wide steps: one more 16x16x32 MFMA whose upper K half
@@ -488,7 +501,7 @@ __device__ __forceinline__ void lds_gemm(const typename O::E *A, const typename 
 #pragma unroll
             for (int q = 0; q < BN; ++q)
                 if ((MT % BM == 0 || m0 + i < MT) && (NT % BN == 0 || n0 + q < NT))
-                    st(m0 + i, n0 + q, d[i][q]);
+                    st(m0 + i, n0 + q, d[i][q].v);
     }
 }
 
@@ -545,33 +558,36 @@ __device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typenam
         auto frag8 = [&](int q, int k) {
             return *reinterpret_cast<const V8 *>(b + q * WN * 16 * P + 32 * k + 8 * lgrp);
         };
-        f32x4 d[BN][BMW];
+        Acc<(K32 > 0 ? 32 : 16)> d[BN][BMW];
 #pragma unroll
         for (int q = 0; q < BN; ++q)
 #pragma unroll
-            for (int i = 0; i < BMW; ++i) d[q][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int i = 0; i < BMW; ++i) d[q][i].v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         V8 cur[BN], nxt[BN];
         if constexpr (K32 > 0) {
 #pragma unroll
             for (int q = 0; q < BN; ++q)
                 if (have(q)) cur[q] = frag8(q, 0);
         }
+        if constexpr (K32 > 0) {
 #pragma unroll
-        for (int k = 0; k < K32; ++k) {
-            if (k + 1 < K32) {
+            for (int k = 0; k < K32; ++k) {
+                if (k + 1 < K32) {
+#pragma unroll
+                    for (int q = 0; q < BN; ++q)
+                        if (have(q)) nxt[q] = frag8(q, k + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int q = 0; q < BN; ++q)
-                    if (have(q)) nxt[q] = frag8(q, k + 1);
+                    if (have(q))
+#pragma unroll
+                        for (int i = 0; i < BMW; ++i)
+                            d[q][i] = O::k32(A.a8[i][k], cur[q], d[q][i]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < BN; ++q) cur[q] = nxt[q];
             }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int q = 0; q < BN; ++q)
-                if (have(q))
-#pragma unroll
-                    for (int i = 0; i < BMW; ++i) d[q][i] = O::k32(A.a8[i][k], cur[q], d[q][i]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int q = 0; q < BN; ++q) cur[q] = nxt[q];
         }
         if constexpr (K16 && K32 > 0) {
             // trailing 16 of K: a 16x16x32 MFMA with the upper K half zero, so that the
@@ -601,7 +617,12 @@ __device__ __forceinline__ void reg_gemm(const RegA<O, BMW, K> &A, const typenam
         }
 #pragma unroll
         for (int q = 0; q < BN; ++q)
-            if (have(q)) st(wn + WN * (j0 + q), d[q]);
+            if (have(q)) {
+                f32x4 out[BMW];
+#pragma unroll
+                for (int i = 0; i < BMW; ++i) out[i] = d[q][i].v;
+                st(wn + WN * (j0 + q), out);
+            }
     }
 }
 
@@ -918,11 +939,11 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     auto vb_tile32 = [&](int mt, int nt) { return vb_row(mt * 32) + vb_col(nt * 32); };
     const int vb_lane32 = vb_row(4 * (lane >> 5)) + vb_col(lane & 31);
 
-    f32x4 acc[G::NYW][G::NACC];
+    Acc<32> acc[G::NYW][G::NACC];
 #pragma unroll
     for (int j = 0; j < G::NYW; ++j)
 #pragma unroll
-        for (int c = 0; c < G::NACC; ++c) acc[j][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < G::NACC; ++c) acc[j][c].v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int g3 = wave / G::KS3, part3 = wave % G::KS3;
     constexpr int K3STEPS = G::K3 / 32, PERK = K3STEPS / G::KS3;
     static_assert(K3STEPS % G::KS3 == 0, "stage-3 K steps must split evenly over KS3 waves");
@@ -1109,7 +1130,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
 #pragma unroll
     for (int j = 0; j < G::NYW; ++j)
 #pragma unroll
-        for (int c = 1; c < G::NACC; ++c) acc[j][0] += acc[j][c];
+        for (int c = 1; c < G::NACC; ++c) acc[j][0].v += acc[j][c].v;
     if constexpr (G::KS3 > 1) {
         __syncthreads();
         float *red = reinterpret_cast<float *>(Ub);
@@ -1117,7 +1138,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
 #pragma unroll
             for (int j = 0; j < G::NYW; ++j)
                 *reinterpret_cast<f32x4 *>(red + (((part3 - 1) * G::G3 + g3) * G::NYW + j) * 256 +
-                                           lane * 4) = acc[j][0];
+                                           lane * 4) = acc[j][0].v;
         }
         __syncthreads();
         if (part3 == 0) {
@@ -1125,7 +1146,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
             for (int j = 0; j < G::NYW; ++j)
 #pragma unroll
                 for (int p = 1; p < G::KS3; ++p)
-                    acc[j][0] += *reinterpret_cast<const f32x4 *>(
+                    acc[j][0].v += *reinterpret_cast<const f32x4 *>(
                         red + (((p - 1) * G::G3 + g3) * G::NYW + j) * 256 + lane * 4);
         }
     }
@@ -1156,7 +1177,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                 const int s = m % G::SC, f = (m / G::SC) % G::FC, t = m / (G::SC * G::FC);
                 if (m < G::M3 && s < SCv && f < FCv && t0 + t < T)
                     static_cast<E *>(y)[size_t(t0 + t) * G::OUT + (f0 + f) * G::SYF +
-                                        (s0 + s) * G::SYS + (l0 + l) * G::SYL] = E(acc[j][0][i]);
+                                        (s0 + s) * G::SYS + (l0 + l) * G::SYL] = E(acc[j][0].v[i]);
             }
         }
     } else {
@@ -1173,7 +1194,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 size_t o;
-                if (y_at(j, i, &o)) epi_put<C.dt>(y, epi_mode, o, acc[j][0][i], a[j][i]);
+                if (y_at(j, i, &o)) epi_put<C.dt>(y, epi_mode, o, acc[j][0].v[i], a[j][i]);
             }
     }
 }
