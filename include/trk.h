@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRK_ABI_VERSION 2
+#define TRK_ABI_VERSION 3
 
 /* Element types of x, y and the cores. */
 enum trk_dtype { TRK_DTYPE_F16 = 0, TRK_DTYPE_BF16 = 1, TRK_DTYPE_F32 = 2 };
@@ -97,6 +97,27 @@ const char *trk_last_error(void);
  * (tr_kernel.py:105-115). */
 int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int dtype,
                     trk_plan **plan);
+
+/* trk_plan_create for cores of rank `core_rank` whose kernels run at rank `rank` >= core_rank.
+ * The packed sections have the kernel rank; trk_pack fills every entry with a ring index at
+ * or past core_rank with zero, so each extra term of the ring trace is zero and the result
+ * is exactly that of the rank-core_rank operator. This lets ranks without compiled MFMA
+ * kernels (4, 12, 24, ...) run the kernels of the next power of two. Replaces the rank
+ * padding of the reference's generic WMMA kernel (tr_ring.cu:348-361, ranks padded to 16).
+ * trk_variant_info.flops and .bytes stay those of the rank-core_rank operator. */
+int trk_plan_create_padded(const int in_modes[3], const int out_modes[3], int core_rank,
+                           int rank, int dtype, trk_plan **plan);
+
+/* Load a variant module and add its variants to `plan`; *added (may be NULL) receives how
+ * many matched the plan's shape, dtype and rank. A variant module is a shared library built
+ * from a generated variant table (factorized_inference/jit.py builds one at prepare time
+ * for a shape that has no compiled MFMA kernels); it is checked against this library's ABI
+ * version and plan layout before it registers anything, and stays loaded for the life of
+ * the process. Its variants may add packed sections, so load modules before
+ * trk_plan_packed_bytes and trk_pack. Replaces the first-use build of the reference's
+ * extension (tr_kernel.py:31-57, torch.utils.cpp_extension.load of tr_ring.cu). Not
+ * thread-safe against other calls on the same plan. */
+int trk_plan_load_module(trk_plan *plan, const char *path, int *added);
 
 /* Free a plan (NULL is a no-op). */
 void trk_plan_destroy(trk_plan *plan);

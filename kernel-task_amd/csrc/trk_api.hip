@@ -4,6 +4,8 @@
 // with a section of the packed-core buffer) and a table of kernel variants with the token
 // counts each one serves. Host-only logic: nothing here calls HIP except trk_pack,
 // trk_forward* and trk_empty_launch.
+#include <dlfcn.h>
+
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
@@ -21,8 +23,10 @@ thread_local char g_error[512] = "";
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
-double chain_flops_per_token(const Plan &p, const Chain &c) {
-    const double R = p.rank;
+// multiply-adds x 2 per token of chain c at ring rank `rank` (the plan's kernel rank for the
+// work its kernels do, its core rank for the algorithmic work)
+double chain_flops_per_token(const Plan &p, const Chain &c, int rank) {
+    const double R = rank;
     const double s1 = double(p.in_features) * c.oF * R * R;
     const double s2 = double(c.nS) * c.nL * c.oF * c.oS * R * R * R;
     const double s3 = double(c.nL) * p.out_features * R * R;
@@ -132,6 +136,11 @@ const char *trk_last_error(void) { return g_error; }
 
 int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int dtype,
                     trk_plan **out) {
+    return trk_plan_create_padded(in_modes, out_modes, rank, rank, dtype, out);
+}
+
+int trk_plan_create_padded(const int in_modes[3], const int out_modes[3], int core_rank,
+                           int rank, int dtype, trk_plan **out) {
     g_error[0] = '\0';
     if (!out || !in_modes || !out_modes)
         return set_error(TRK_ERR_INVALID, "trk_plan_create: null argument");
@@ -139,7 +148,10 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     for (int m = 0; m < 3; ++m)
         if (in_modes[m] <= 0 || out_modes[m] <= 0)
             return set_error(TRK_ERR_INVALID, "trk_plan_create: modes must be positive");
-    if (rank <= 0) return set_error(TRK_ERR_INVALID, "trk_plan_create: rank must be positive");
+    if (core_rank <= 0) return set_error(TRK_ERR_INVALID, "trk_plan_create: rank must be positive");
+    if (rank < core_rank)
+        return set_error(TRK_ERR_INVALID, "trk_plan_create: kernel rank %d below the cores' rank %d",
+                         rank, core_rank);
     if (dtype != TRK_DTYPE_F16 && dtype != TRK_DTYPE_BF16 && dtype != TRK_DTYPE_F32)
         return set_error(TRK_ERR_INVALID, "trk_plan_create: unknown dtype %d", dtype);
     const long long in_f = 1LL * in_modes[0] * in_modes[1] * in_modes[2];
@@ -152,6 +164,7 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     std::copy(in_modes, in_modes + 3, p->in_modes);
     std::copy(out_modes, out_modes + 3, p->out_modes);
     p->rank = rank;
+    p->core_rank = core_rank;
     p->dtype = dtype;
     p->elem = dtype == TRK_DTYPE_F32 ? 4 : 2;
     p->in_features = int(in_f);
@@ -166,7 +179,7 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     for (int o = 0; o < 6; ++o) {
         Chain c;
         describe_chain(in_modes, out_modes, rank, kOrders[o], &c);
-        const double fl = chain_flops_per_token(*p, c);
+        const double fl = chain_flops_per_token(*p, c, rank);
         if (o == 0 || fl < best_flops * (1.0 - 1e-9)) {
             best = o;
             best_flops = fl;
@@ -209,6 +222,27 @@ int trk_plan_create(const int in_modes[3], const int out_modes[3], int rank, int
     return TRK_OK;
 }
 
+int trk_plan_load_module(trk_plan *plan, const char *path, int *added) {
+    if (added) *added = 0;
+    if (!plan || !path) return set_error(TRK_ERR_INVALID, "trk_plan_load_module: null argument");
+    // loaded once per process and never closed: the plan's variants point into the module
+    void *h = dlopen(path, RTLD_NOW | RTLD_LOCAL);
+    if (!h) return set_error(TRK_ERR_INVALID, "trk_plan_load_module: %s", dlerror());
+    auto abi = reinterpret_cast<int (*)()>(dlsym(h, kModuleAbi));
+    auto size = reinterpret_cast<ModuleSizeFn>(dlsym(h, kModulePlanSize));
+    auto reg = reinterpret_cast<ModuleRegisterFn>(dlsym(h, kModuleRegister));
+    if (!abi || !size || !reg)
+        return set_error(TRK_ERR_INVALID, "trk_plan_load_module: %s is not a variant module", path);
+    if (abi() != TRK_ABI_VERSION || size() != sizeof(Plan))
+        return set_error(TRK_ERR_INVALID,
+                         "trk_plan_load_module: %s was built for ABI %d, plan size %zu (this "
+                         "library: ABI %d, plan size %zu)", path, abi(), size(), TRK_ABI_VERSION,
+                         sizeof(Plan));
+    const int n = reg(as_plan(plan));
+    if (added) *added = n;
+    return TRK_OK;
+}
+
 void trk_plan_destroy(trk_plan *plan) { delete as_plan(plan); }
 
 size_t trk_plan_packed_bytes(const trk_plan *plan) {
@@ -246,9 +280,11 @@ int trk_plan_describe(const trk_plan *plan, int variant, int tokens, trk_variant
     info->lds_bytes = v.lds_bytes;
     info->t_min = v.t_min;
     info->t_max = v.t_max;
-    info->flops = chain_flops_per_token(p, c) * tokens;
+    // algorithmic work of the cores' rank (a padded plan's kernels do more, on zeros)
+    info->flops = chain_flops_per_token(p, c, p.core_rank) * tokens;
     double params = 0.0;
-    for (int m = 0; m < 3; ++m) params += double(p.rank) * p.rank * p.in_modes[m] * p.out_modes[m];
+    for (int m = 0; m < 3; ++m)
+        params += double(p.core_rank) * p.core_rank * p.in_modes[m] * p.out_modes[m];
     info->bytes = double(p.elem) * (params + double(tokens) * (p.in_features + p.out_features));
     info->packed_offset[0] = c.offF;
     info->packed_offset[1] = c.offS;

@@ -69,6 +69,7 @@ struct Variant {
 
 struct Plan {
     int in_modes[3], out_modes[3], rank, dtype, elem;
+    int core_rank;  // rank of the cores trk_pack reads (<= rank; the rest is zero padding)
     int in_features, out_features;
     int nchains;
     Chain chains[kMaxChains];
@@ -86,6 +87,14 @@ void describe_chain(const int in_modes[3], const int out_modes[3], int rank, con
                     Chain *chain);
 // index of the plan's chain with this order and K-order groups, added if new (-1: full)
 int plan_chain(Plan *plan, const int order[3], int sg, int lg, int sfrag);
+
+// Entry points a variant module (a generated table built at prepare time) exports, and the
+// layout check its loader applies: the module's sizeof(Plan) must equal the library's.
+using ModuleRegisterFn = int (*)(Plan *plan);
+using ModuleSizeFn = size_t (*)();
+constexpr const char *kModuleRegister = "trk_module_register";
+constexpr const char *kModulePlanSize = "trk_module_plan_size";
+constexpr const char *kModuleAbi = "trk_module_abi";
 
 // kernels and their launchers
 int launch_pack(const Plan &plan, const void *g1, const void *g2, const void *g3, void *packed,

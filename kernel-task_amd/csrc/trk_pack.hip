@@ -28,7 +28,7 @@ __device__ inline size_t core_index(int alpha, int o, int i, int beta, int O, in
 }
 
 struct PackArgs {
-    int R, forward;
+    int R, Rc, forward;  // kernel rank; rank of the cores read (ring indices >= Rc pack zero)
     int nF, nS, nL, oF, oS, oL, KF, K2, sg, lg, sfrag;
     size_t nFk, nSk, nLk;  // element counts of the three sections
 };
@@ -51,9 +51,9 @@ __global__ void __launch_bounds__(256) pack_chain_kernel(const W *__restrict__ g
             const int r1 = int(rest % R);
             const int f = int(rest / R);
             W v = W(0);
-            if (iF < a.nF)
-                v = gF[a.forward ? core_index(r1, f, iF, r2, a.oF, a.nF, R)
-                                 : core_index(r2, f, iF, r1, a.oF, a.nF, R)];
+            if (iF < a.nF && r1 < a.Rc && r2 < a.Rc)
+                v = gF[a.forward ? core_index(r1, f, iF, r2, a.oF, a.nF, a.Rc)
+                                 : core_index(r2, f, iF, r1, a.oF, a.nF, a.Rc)];
             Fk[d] = v;
         } else if (d < a.nFk + a.nSk) {
             const size_t e = d - a.nFk;
@@ -72,8 +72,9 @@ __global__ void __launch_bounds__(256) pack_chain_kernel(const W *__restrict__ g
             if (k < a.nS * R && s < a.oS) {
                 const int span = a.sg * a.nS, rem = k % span;
                 const int iS = rem / a.sg, r2 = k / span * a.sg + rem % a.sg;
-                v = gS[a.forward ? core_index(r2, s, iS, r3, a.oS, a.nS, R)
-                                 : core_index(r3, s, iS, r2, a.oS, a.nS, R)];
+                if (r2 < a.Rc && r3 < a.Rc)
+                    v = gS[a.forward ? core_index(r2, s, iS, r3, a.oS, a.nS, a.Rc)
+                                     : core_index(r3, s, iS, r2, a.oS, a.nS, a.Rc)];
             }
             Sk[e] = v;
         } else {
@@ -83,8 +84,11 @@ __global__ void __launch_bounds__(256) pack_chain_kernel(const W *__restrict__ g
             size_t rest = e / (size_t(R) * R);
             const int l = int(rest % a.oL);
             const int iL = int(rest / a.oL);
-            Lk[e] = gL[a.forward ? core_index(r3, l, iL, r1, a.oL, a.nL, R)
-                                 : core_index(r1, l, iL, r3, a.oL, a.nL, R)];
+            W v = W(0);
+            if (r1 < a.Rc && r3 < a.Rc)
+                v = gL[a.forward ? core_index(r3, l, iL, r1, a.oL, a.nL, a.Rc)
+                                 : core_index(r1, l, iL, r3, a.oL, a.nL, a.Rc)];
+            Lk[e] = v;
         }
     }
 }
@@ -96,6 +100,7 @@ int pack_all(const Plan &plan, const void *const g[3], void *packed, hipStream_t
         const Chain &c = plan.chains[ci];
         PackArgs a;
         a.R = c.R;
+        a.Rc = plan.core_rank;
         a.forward = c.forward;
         a.nF = c.nF;
         a.nS = c.nS;

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libtrk.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 KERNEL_GENERIC, KERNEL_MFMA = 0, 1
@@ -55,6 +55,9 @@ SIGNATURES = {
     "trk_abi_version": (_c_int, []),
     "trk_last_error": (_c_char_p, []),
     "trk_plan_create": (_c_int, [_int3, _int3, _c_int, _c_int, ctypes.POINTER(_c_void_p)]),
+    "trk_plan_create_padded": (_c_int, [_int3, _int3, _c_int, _c_int, _c_int,
+                                        ctypes.POINTER(_c_void_p)]),
+    "trk_plan_load_module": (_c_int, [_c_void_p, _c_char_p, ctypes.POINTER(_c_int)]),
     "trk_plan_destroy": (None, [_c_void_p]),
     "trk_plan_packed_bytes": (_c_size_t, [_c_void_p]),
     "trk_plan_variant_count": (_c_int, [_c_void_p]),
@@ -112,15 +115,20 @@ def check(status: int) -> None:
 
 
 class Plan:
-    """Owner of one trk_plan (host memory only)."""
+    """Owner of one trk_plan (host memory only). kernel_rank > rank makes a padded plan
+    (trk_plan_create_padded): its kernels run at kernel_rank on zero-padded cores."""
 
-    def __init__(self, input_modes, output_modes, rank: int, dtype_code: int):
+    def __init__(self, input_modes, output_modes, rank: int, dtype_code: int,
+                 kernel_rank: int | None = None):
         lib = load()
         handle = _c_void_p()
-        check(lib.trk_plan_create(_int3(*input_modes), _int3(*output_modes), int(rank),
-                                  int(dtype_code), ctypes.byref(handle)))
+        self.rank = int(rank)
+        self.kernel_rank = int(kernel_rank or rank)
+        check(lib.trk_plan_create_padded(_int3(*input_modes), _int3(*output_modes), self.rank,
+                                         self.kernel_rank, int(dtype_code), ctypes.byref(handle)))
         self._lib = lib
         self.handle = handle.value
+        self.modules: list[str] = []
 
     def __del__(self):
         handle, self.handle = getattr(self, "handle", None), None
@@ -149,3 +157,15 @@ class Plan:
 
     def set_variant(self, t_min: int, t_max: int, variant: int) -> None:
         check(self._lib.trk_plan_set_variant(self.handle, int(t_min), int(t_max), int(variant)))
+
+    @property
+    def has_mfma(self) -> bool:
+        return any(v["kind"] == "mfma" for v in self.variants())
+
+    def load_module(self, path) -> int:
+        """Add the variants of a variant module (trk_plan_load_module); returns how many.
+        Call before packing: the variants may add packed sections."""
+        added = _c_int(0)
+        check(self._lib.trk_plan_load_module(self.handle, str(path).encode(), ctypes.byref(added)))
+        self.modules.append(str(path))
+        return added.value

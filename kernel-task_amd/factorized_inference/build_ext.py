@@ -97,7 +97,7 @@ def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Pa
     RESOURCES.write_text(json.dumps(resources, indent=0, sort_keys=True) + "\n")
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objects)]
+           *map(str, objects), "-ldl"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

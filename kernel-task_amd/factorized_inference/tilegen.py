@@ -636,6 +636,26 @@ def emit(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fal
     return "\n".join(lines)
 
 
+def emit_module(shape: ShapeDecl) -> str:
+    """Source of a variant module for one shape that the library has no compiled tables for:
+    the shape's candidate tiles with rule-based token ranges (untuned), and the entry points
+    trk_plan_load_module looks up (include/trk.h). Built at prepare time by jit.py."""
+    text = emit(shape, tuned={})
+    table_fn = _fn_name(shape)
+    # the table's registration function stays internal to the module
+    text = text.replace(f"int {table_fn}(Plan *plan) {{", "int module_table(Plan *plan) {")
+    # (modules are compiled with hidden visibility: only these three entry points export)
+    export = 'extern "C" __attribute__((visibility("default")))'
+    text = text.replace("}  // namespace trk\n", "}  // namespace trk\n\n"
+                        f"{export} int trk_module_register(trk::Plan *plan) {{\n"
+                        "    return trk::module_table(plan);\n}\n"
+                        f"{export} size_t trk_module_plan_size() {{ return sizeof(trk::Plan); }}\n"
+                        f"{export} int trk_module_abi() {{ return TRK_ABI_VERSION; }}\n")
+    return text.replace("// Generated by kernel-task_amd/factorized_inference/tilegen.py; do not edit.",
+                        "// Variant module generated at prepare time by "
+                        "kernel-task_amd/factorized_inference/jit.py (tilegen.emit_module).")
+
+
 def emit_index(shapes: list[ShapeDecl]) -> str:
     lines = [
         "// Generated by kernel-task_amd/factorized_inference/tilegen.py; do not edit.",

@@ -4,6 +4,9 @@ Mirrors src/factorized_inference/tr_kernel.py of the reference (PreparedTRKernel
 prepare time, a tiling/variant choice per token count) with its own mechanics:
 
   prepare  trk_plan_create picks the contraction order(s) and kernel variants for the shape;
+           a 16-bit shape without compiled MFMA tables gets a variant module built for it
+           (jit.py: the generator's table compiled once, cached), at the next power-of-two
+           kernel rank when the cores' rank has none (zero-padded ring links, exact);
            trk_pack packs the cores into one device buffer (no dense W, padding only)
   call     one C++ call per input (_trktorch.forward): check x, allocate the output with
            torch's caching allocator, trk_forward on the caller's current stream. No
@@ -22,11 +25,12 @@ token count to that variant of the plan (indices from `PreparedTRKernel.variants
 from __future__ import annotations
 
 import os
+import warnings
 from typing import Sequence
 
 import torch
 
-from . import _lib
+from . import _lib, jit, tilegen
 from .reference import TRSpec, _validate_cores
 
 _DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16,
@@ -61,6 +65,36 @@ def _torch_call():
     return _trktorch
 
 
+def make_plan(spec: TRSpec, dtype: torch.dtype) -> _lib.Plan:
+    """The plan of one operator: the library's own variant tables; for fp16/bf16 shapes
+    without MFMA variants, a plan at the MFMA kernel rank (trk_plan_create_padded when the
+    cores' rank is not a power of two >= 8) with a variant module built for the shape
+    (jit.build_module). Shapes the generator has no tile for, fp32, and TRK_JIT=0 keep the
+    generic HIP kernel."""
+    code = _DTYPES[dtype]
+    plan = _lib.Plan(spec.input_modes, spec.output_modes, spec.rank, code)
+    if dtype is torch.float32 or plan.has_mfma or not jit.enabled():
+        return plan
+    krank = jit.kernel_rank(spec.rank)
+    if krank is None:
+        return plan
+    padded = plan if krank == spec.rank else _lib.Plan(
+        spec.input_modes, spec.output_modes, spec.rank, code, kernel_rank=krank)
+    if not padded.has_mfma:
+        shape = tilegen.ShapeDecl("prepared", tuple(spec.input_modes), tuple(spec.output_modes),
+                                  krank, "f16" if dtype is torch.float16 else "bf16")
+        try:
+            path = jit.build_module(shape)
+        except (OSError, RuntimeError) as exc:
+            warnings.warn(f"no MFMA variant module for {shape.key} ({exc}); the generic "
+                          "kernel serves this shape", RuntimeWarning)
+            return plan
+        if path is None:
+            return plan
+        padded.load_module(path)
+    return padded if padded.has_mfma else plan
+
+
 def current_stream_handle(device_index: int) -> int:
     """hipStream_t of torch's current stream on `device_index`, as an integer."""
     return _raw_stream(device_index)
@@ -88,7 +122,7 @@ class PreparedTRKernel:
         self.device_index = device.index if device.index is not None else torch.cuda.current_device()
         self.in_features = spec.in_features
         self.out_features = spec.out_features
-        self.plan = _lib.Plan(spec.input_modes, spec.output_modes, spec.rank, _DTYPES[dtype])
+        self.plan = make_plan(spec, dtype)
         forced = os.environ.get("TRK_VARIANT")
         if forced is not None:
             self.plan.set_variant(1, 1 << 30, int(forced))

@@ -64,6 +64,29 @@ int main(void) {
           "zero mode rejected");
     CHECK(trk_plan_create(in_modes, out_modes, 8, 7, &bad) == TRK_ERR_INVALID, "bad dtype");
 
+    /* padded plans: rank 4 cores on the rank-8 kernels; the work reported stays rank 4's */
+    trk_plan *padded = NULL, *small = NULL;
+    CHECK(trk_plan_create_padded(in_modes, out_modes, 8, 4, TRK_DTYPE_F16, &bad) ==
+              TRK_ERR_INVALID && bad == NULL,
+          "kernel rank below the cores' rank rejected");
+    CHECK(trk_plan_create_padded(in_modes, out_modes, 4, 8, TRK_DTYPE_F16, &padded) == TRK_OK,
+          "padded plan");
+    CHECK(trk_plan_create(in_modes, out_modes, 4, TRK_DTYPE_F16, &small) == TRK_OK, "rank-4 plan");
+    trk_variant_info pinfo, sinfo;
+    CHECK(trk_plan_describe(padded, -1, 1, &pinfo) == TRK_OK &&
+              trk_plan_describe(small, 0, 1, &sinfo) == TRK_OK,
+          "describe padded and unpadded");
+    CHECK(pinfo.kind == TRK_KERNEL_MFMA, "the padded plan runs the rank-8 MFMA kernels");
+    CHECK(pinfo.bytes == sinfo.bytes && pinfo.flops < info.flops, "padded plan reports rank 4's work");
+    CHECK(trk_plan_packed_bytes(padded) == trk_plan_packed_bytes(plan), "sections of the kernel rank");
+    int added = -1;
+    CHECK(trk_plan_load_module(padded, "/nonexistent/module.so", &added) == TRK_ERR_INVALID &&
+              added == 0 && strlen(trk_last_error()) > 0,
+          "a missing module is an error");
+    CHECK(trk_plan_load_module(padded, NULL, NULL) == TRK_ERR_INVALID, "null module path");
+    trk_plan_destroy(padded);
+    trk_plan_destroy(small);
+
     trk_plan_destroy(plan);
     trk_plan_destroy(NULL);
     printf("all checks passed\n");

@@ -1,0 +1,72 @@
+"""Prepare-time variant modules (factorized_inference/jit.py) and padded plans, host side:
+the kernel-rank rule, the generated module source, building and caching, loading into a plan
+through trk_plan_load_module, and the work a padded plan reports. No GPU needed (hipcc
+cross-compiles; dlopen of a HIP module works without a device)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from factorized_inference import TRSpec, _lib, jit, tilegen
+from factorized_inference.tr_kernel import make_plan
+from jit_shapes import JIT_SHAPES
+
+
+def test_kernel_rank_rule():
+    assert [jit.kernel_rank(r) for r in (1, 4, 7, 8)] == [8] * 4
+    assert [jit.kernel_rank(r) for r in (9, 12, 16)] == [16] * 3
+    assert [jit.kernel_rank(r) for r in (17, 24, 32)] == [32] * 3
+    assert jit.kernel_rank(33) is None
+
+
+def test_module_source_keeps_only_ranged_tiles():
+    shape = tilegen.ShapeDecl("t", (4, 6, 8), (6, 4, 8), 16, "f16")
+    src = jit.module_source(shape)
+    entries = [ln for ln in src.splitlines() if "TRK_ENTRY(" in ln]
+    assert entries and not any(ln.split("//")[0].rstrip().endswith(", 0, 0)") for ln in entries)
+    for symbol in ("trk_module_register", "trk_module_plan_size", "trk_module_abi"):
+        assert symbol in src
+    # no tile fits this shape (12 inputs, no contiguous first-core order): no module
+    assert jit.module_source(tilegen.ShapeDecl("t", (2, 3, 2), (2, 4, 3), 8, "f16")) is None
+
+
+def test_module_is_built_once_and_reused():
+    shape = tilegen.ShapeDecl("t", (4, 6, 8), (6, 4, 8), 8, "f16")
+    path = jit.build_module(shape)
+    assert path is not None and path.exists() and path == jit.module_path(shape)
+    stamp = path.stat().st_mtime_ns
+    assert jit.build_module(shape) == path and path.stat().st_mtime_ns == stamp
+
+
+@pytest.mark.parametrize("ins,outs,rank,dtype", JIT_SHAPES)
+def test_undeclared_shapes_get_mfma_variants(ins, outs, rank, dtype):
+    spec = TRSpec(ins, outs, rank)
+    dt = getattr(torch, dtype)
+    plan = make_plan(spec, dt)
+    assert plan.has_mfma
+    assert plan.kernel_rank == jit.kernel_rank(rank)
+    for tokens in (1, 8, 64, 1000):
+        assert plan.describe(-1, tokens)["kind"] == "mfma", tokens
+    # the work reported is the rank-`rank` operator's, whatever rank the kernels run at
+    unpadded = _lib.Plan(ins, outs, rank, 0 if dt is torch.float16 else 1)
+    for tokens in (1, 7):
+        assert plan.describe(-1, tokens)["bytes"] == unpadded.describe(0, tokens)["bytes"]
+    params = sum(rank * rank * i * o for i, o in zip(ins, outs))
+    assert plan.describe(-1, 1)["bytes"] == 2.0 * (params + spec.in_features + spec.out_features)
+
+
+def test_fp32_and_disabled_jit_keep_the_generic_kernel(monkeypatch):
+    spec = TRSpec((4, 6, 8), (6, 4, 8), 8)
+    assert not make_plan(spec, torch.float32).has_mfma
+    monkeypatch.setenv("TRK_JIT", "0")
+    assert not make_plan(spec, torch.float16).has_mfma
+
+
+def test_loader_rejects_other_libraries():
+    from factorized_inference import _trkcall
+
+    plan = _lib.Plan((4, 6, 8), (6, 4, 8), 8, _lib.DTYPE_F16)
+    with pytest.raises(_lib.TrkError, match="not a variant module"):
+        plan.load_module(_trkcall.__file__)
+    with pytest.raises(_lib.TrkError):
+        plan.load_module("/nonexistent/trk_mod.so")
