@@ -348,13 +348,11 @@ struct Geo {
 };
 
 
-// Wait for every outstanding global load of this wave.
-__device__ inline void wait_loads() { __builtin_amdgcn_s_waitcnt(0); }
-
 // LDS <- global through VGPRs for NB blocks of BLOCK 16-byte vectors, spread over the NT
 // threads of a workgroup: block b is read from src + b * stride (vectors), its first `valid`
-// vectors from memory and the rest zero. issue() starts every read of the copy; commit(),
-// after wait_loads(), writes the LDS as rows of ROW vectors at a pitch of PITCH vectors.
+// vectors from memory and the rest zero. issue() starts every read of the copy; commit()
+// writes the LDS as rows of ROW vectors at a pitch of PITCH vectors (the compiler waits for
+// exactly the loads whose registers it stores).
 template <int NB, int BLOCK, int ROW, int NT, int PITCH>
 struct RegCopy {
     static_assert(BLOCK % ROW == 0, "a copy block holds whole LDS rows");
@@ -823,13 +821,14 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         issue_l(iL0);
         issue_x(iL0);
     };
+    // The commits wait only for the loads whose registers they store: the compiler's
+    // per-register wait counts (loads complete in issue order), so loads issued after them
+    // (the register-resident slices in the prologue) stay in flight.
     auto commit_l = [&](int buf) TRK_INLINE {  // into buffer `buf` of Ls
-        wait_loads();
         cL.commit(Ls + buf * G::szLs);
     };
     auto commit_x = [&](int iL0, int buf) TRK_INLINE {  // into buffer `buf` of Xs
         E *xs = Xs + buf * G::szXs;
-        wait_loads();
         if constexpr (G::XROW) {
 #pragma unroll
             for (int j = 0; j < XREG; ++j) {
@@ -846,7 +845,6 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                 for (int j = 0; j < XREG; ++j)
                     xb[j] = j0 + j < XPER ? x_scatter_load(tid + (j0 + j) * G::NT)
                                           : make_uint4(0u, 0u, 0u, 0u);
-                wait_loads();
 #pragma unroll
                 for (int j = 0; j < XREG; ++j)
                     if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * G::NT, xb[j], iL0, xs);
@@ -865,6 +863,11 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     constexpr int HW = G::NW / 2;
     const int wm2 = G::TAIL ? (wave < HW ? wave : HW + (wave - HW) / G::TAILJ) : wave % G::WM2;
     const int wn2 = G::TAIL ? (wave < HW ? 0 : (wave - HW) % G::TAILJ) : wave / G::WM2;
+    // LDS-staged tiles issue the first step's last-core slice and x first: the commit and
+    // stage 1 need them, while the core slices committed after them can still be in flight.
+    // (Register-resident tiles keep the slices first: their prologue is bound by the CU's
+    // vector-memory rate, and measured 1-2 % faster in that order.)
+    if constexpr (!G::WIDE) issue_step(0);
     // the first- and second-core slices stay resident for the whole call
     RegA<O, G::BM1, G::KF> fa;
     std::conditional_t<G::W32, RegA32<O, G::BM2, G::K2>, RegA<O, G::BM2, G::K2>> sa;
@@ -880,7 +883,7 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
         cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
     }
-    issue_step(0);
+    if constexpr (G::WIDE) issue_step(0);
     // While the loads fly: zero what no load writes. The contiguous-iF loader writes all of
     // Xs; the scatter loader leaves the K padding, the rows iS >= nS and the rows of absent
     // tokens (TT > 1) to this fill, which writes only those.
