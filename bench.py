@@ -178,6 +178,56 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
     return results
 
 
+def xcd_local_figure(steps: int, warmup: int) -> dict | None:
+    """The headline workload on the plan's XCD-local variant (PreparedTRKernel.use_xcd_local:
+    every workgroup on one XCD) against the default variant, as a paired comparison: both
+    warmed for ~0.3 s, then 9 alternating blocks of `steps` calls each. Checked like every
+    case, with the HBM traffic its counter runs measured (profiles/traffic_r8_t1_xl.json)."""
+    import torch
+
+    from factorized_inference import TRSpec, make_cores, prepare_optimized, tr_forward_reference
+    from factorized_inference import measure as m
+
+    label, ins, outs, rank, dt, init, _ = CASES[0]
+    spec = TRSpec(ins, outs, rank)
+    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=0, init=init)
+    base = prepare_optimized(cores, spec)
+    run = prepare_optimized(cores, spec)
+    if not run.use_xcd_local():
+        return None
+    x = torch.randn(1, spec.in_features, generator=torch.Generator(device="cuda").manual_seed(1),
+                    device="cuda", dtype=torch.float16)
+    ours = lambda: run(x)  # noqa: E731
+    default = lambda: base(x)  # noqa: E731
+    t_end = time.perf_counter() + 0.3
+    while time.perf_counter() < t_end:
+        for _ in range(max(warmup, 50)):
+            ours()
+            default()
+        m.synchronize()
+    blocks, default_blocks = [], []
+    for _ in range(9):
+        blocks += m.stream_us(ours, steps, blocks=1)
+        default_blocks += m.stream_us(default, steps, blocks=1)
+    y = run(x).float()
+    ref = tr_forward_reference(x.float(), [c.float() for c in cores], spec)
+    diff = (y - ref).abs()
+    tol = TOLERANCE[dt]
+    ok = (bool((diff <= tol + tol * ref.abs()).all().item()) and bool(torch.isfinite(y).all())
+          and diff.max().item() <= 1e-2 * ref.abs().max().item())
+    out = {"variant": run.selected(1)["name"], "value": statistics.median(blocks),
+           "default_variant": base.selected(1)["name"],
+           "default_value": statistics.median(default_blocks), "unit": "us/call",
+           "protocol": f"median of 9 blocks of {steps} calls, alternating with the default",
+           "passed": ok, "max_abs_err_vs_fp32": diff.max().item()}
+    path = ROOT / "profiles" / "traffic_r8_t1_xl.json"
+    if path.exists():
+        t = json.loads(path.read_text())
+        out.update(traffic=t.get("hbm_bytes_per_launch"), traffic_kernel=t.get("kernel"),
+                   traffic_ratio_to_algorithmic=t.get("ratio_to_algorithmic"))
+    return out
+
+
 def cpu_baseline(seconds: float) -> dict:
     """The reference CPU path, config 1 (1920->2880, R8, fp32, T=1, per-core sigma, seed 0),
     timed on this host: the oracle's numpy port of the reference's three contractions
@@ -255,20 +305,26 @@ def _cpu_model() -> str:
             f"stepping {fields.get('stepping', '?')})")
 
 
-def traffic_probe(calls: int) -> None:
-    """Workload for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs: `calls` launches of
-    the headline kernel, then a plain 512 MiB device copy (5 launches; larger than every L2
-    and the 256 MB MALL, so its reads come from HBM) whose counters give the scale factor
-    between counted and actual bytes."""
+def traffic_probe(calls: int, case: str = "r8:1") -> None:
+    """Workload of the rocprofv3 --pmc runs: `calls` launches of one case's kernel (`case` is
+    "label:tokens" of CASES; the headline r8:1 by default), then a plain 512 MiB device copy
+    (5 launches; larger than every L2 and the 256 MB MALL, so its reads come from HBM) whose
+    counters give the scale factor between counted and actual bytes."""
     import torch
 
     from factorized_inference import TRSpec, make_cores, prepare_optimized
 
-    spec = TRSpec()
-    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=0)
+    label, _, tok = case.partition(":")
+    found = [c for c in CASES if c[0] == label]
+    if not found or not tok.isdigit() or int(tok) < 1:
+        raise SystemExit(f"--probe-case wants label:tokens with a label of {[c[0] for c in CASES]}")
+    _, ins, outs, rank, dt, init, _ = found[0]
+    T, dtype = int(tok), getattr(torch, dt)
+    spec = TRSpec(ins, outs, rank)
+    cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init=init)
     run = prepare_optimized(cores, spec)
-    x = torch.randn(1, spec.in_features, generator=torch.Generator(device="cuda").manual_seed(1),
-                    device="cuda", dtype=torch.float16)
+    x = torch.randn(T, spec.in_features, generator=torch.Generator(device="cuda").manual_seed(1),
+                    device="cuda", dtype=dtype)
     for _ in range(calls):
         run(x)
     src = torch.ones(256 << 20, dtype=torch.float16, device="cuda")
@@ -276,7 +332,7 @@ def traffic_probe(calls: int) -> None:
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"traffic probe: {calls} x {run.selected(1)['name']}, 5 x copy of "
+    print(f"traffic probe: {calls} x {run.selected(T)['name']} ({label}, T={T}), 5 x copy of "
           f"{src.numel() * 2} bytes", flush=True)
 
 
@@ -347,14 +403,16 @@ def main() -> int:
                          "default kernel-argument placement")
     ap.add_argument("--runtime-default-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="CALLS",
-                    help="only run the workload of the HBM-traffic counter runs")
+                    help="only run the workload of the counter (rocprofv3 --pmc) runs")
+    ap.add_argument("--probe-case", default="r8:1", metavar="LABEL:TOKENS",
+                    help="case of the --traffic-probe workload (default r8:1, the headline)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         return 2
     if args.traffic_probe:
-        traffic_probe(args.traffic_probe)
+        traffic_probe(args.traffic_probe, args.probe_case)
         return 0
     if args.runtime_default_child:
         return runtime_default_child(args.steps, args.warmup)
@@ -387,7 +445,10 @@ def main() -> int:
             cases += measure_case(label, ins, outs, rank, dt, init, tokens, args.steps,
                                   args.warmup, headline=(i == 0), profile_kernels=profile)
         floors = m.floors(_lib.load(), profiler=profile)
+        xcd_local = None if args.headline_only else xcd_local_figure(args.steps, args.warmup)
     failed = [f"{c['case']} T={c['tokens']}" for c in cases if not c["passed"]]
+    if xcd_local is not None and not xcd_local["passed"]:
+        failed.append("r8 T=1 XCD-local")
     if failed:
         log(f"results outside the acceptance tolerance: {', '.join(failed)}; no bench line")
         return 1
@@ -432,6 +493,7 @@ def main() -> int:
                    "runtime_default": default_runtime},
         "dense_stream_us": head["dense_stream_us"],
         "roofline": roof,
+        "xcd_local": xcd_local,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
         "floors": floors,
         "cases": cases,

@@ -191,7 +191,10 @@ def main() -> int:
         for shape in tilegen.DECLARED:
             if wanted and shape.key not in wanted:
                 continue
+            prev = result.get(shape.key) or tilegen.load_tuned().get(shape.key) or {}
             result[shape.key], raw[shape.key] = tune_shape(shape, args.seconds_per_shape)
+            if prev.get("extra"):  # index-only alternatives outlive a retune
+                result[shape.key]["extra"] = prev["extra"]
             for path, data in ((args.out, result), (args.measurements, raw)):
                 path.parent.mkdir(parents=True, exist_ok=True)
                 path.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")

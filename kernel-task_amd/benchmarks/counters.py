@@ -1,0 +1,124 @@
+"""Summaries of `rocprofv3 --pmc ... -f csv` runs of `bench.py --traffic-probe`.
+
+    # HBM traffic per launch (one FETCH_SIZE run and one WRITE_SIZE run of the same probe)
+    python kernel-task_amd/benchmarks/counters.py traffic --fetch DIR --write DIR --out FILE.json
+    # per-dispatch means of every counter of the probed kernel, one or more runs
+    python kernel-task_amd/benchmarks/counters.py means DIR [DIR ...]
+
+A probe run (bench.py --traffic-probe CALLS) launches one tensor-ring kernel CALLS times and
+then copies a 512 MiB buffer 5 times. The copy is larger than every L2 and the 256 MB MALL,
+so its bytes all cross from HBM: the counted KiB per copy against the 512 MiB it moves give
+the scale between a counter and bytes (FETCH_SIZE counts 2x on MI355X at this writing,
+WRITE_SIZE 1x), which is applied to the kernel's per-dispatch mean.
+
+Role of the reference's tools/measure_kernels.py (profiler-derived rates of the fused kernel)
+for the counters it has no equivalent of on its hardware.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import re
+import sys
+from collections import defaultdict
+from pathlib import Path
+
+COPY_BYTES = 512 << 20  # bench.py traffic_probe: torch.ones(256 << 20, float16) copied
+
+
+def _rows(run_dir: Path) -> list[dict]:
+    files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {run_dir}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def kernel_label(name: str) -> str | None:
+    """'ring3<KCfg fields>' for a tensor-ring kernel, 'copy' for the runtime's buffer copy,
+    None for anything else (allocation fills, packing, random inputs)."""
+    if "ring3_mfma" in name:
+        m = re.search(r"KCfg\{([^}]*)\}", name)
+        return "ring3<" + (m.group(1).replace(" ", "") if m else "?") + ">"
+    if "ring3_generic" in name:
+        return "ring3_generic"
+    if "copyBuffer" in name:
+        return "copy"
+    return None
+
+
+def means(run_dir: Path) -> dict[str, dict[str, dict]]:
+    """{kernel label: {counter: {"dispatches": n, "mean": per-dispatch mean}}}."""
+    acc: dict = defaultdict(lambda: defaultdict(list))
+    for r in _rows(run_dir):
+        label = kernel_label(r["Kernel_Name"])
+        if label is not None:
+            acc[label][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return {k: {c: {"dispatches": len(v), "mean": sum(v) / len(v)} for c, v in cs.items()}
+            for k, cs in acc.items()}
+
+
+def probed_kernel(m: dict) -> str:
+    """The tensor-ring kernel a probe launched (the most dispatched one)."""
+    ring = [k for k in m if k.startswith("ring3")]
+    if not ring:
+        raise SystemExit("no tensor-ring kernel in the run")
+    return max(ring, key=lambda k: max(v["dispatches"] for v in m[k].values()))
+
+
+def traffic(fetch_dir: Path, write_dir: Path, algorithmic_bytes: float | None) -> dict:
+    out = {"counters": {}}
+    total = 0.0
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        m = means(d)
+        kernel = probed_kernel(m)
+        ring = m[kernel][counter]
+        copy = m["copy"][counter]
+        scale = COPY_BYTES / (copy["mean"] * 1024.0)
+        nbytes = ring["mean"] * 1024.0 * scale
+        out["kernel"] = kernel
+        out["counters"][counter] = {
+            "ring_kib_per_dispatch_mean": ring["mean"], "ring_dispatches": ring["dispatches"],
+            "copy_kib_per_dispatch_mean": copy["mean"], "copy_dispatches": copy["dispatches"],
+            "copy_bytes_actual": COPY_BYTES, "scale": scale, "ring_bytes_per_dispatch": nbytes}
+        total += nbytes
+    out["hbm_bytes_per_launch"] = total
+    if algorithmic_bytes:
+        out["algorithmic_bytes_per_launch"] = algorithmic_bytes
+        out["ratio_to_algorithmic"] = total / algorithmic_bytes
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("--fetch", type=Path, required=True)
+    t.add_argument("--write", type=Path, required=True)
+    t.add_argument("--algorithmic-bytes", type=float, default=None)
+    t.add_argument("--workload", default="")
+    t.add_argument("--out", type=Path)
+    mp = sub.add_parser("means")
+    mp.add_argument("dirs", type=Path, nargs="+")
+    args = ap.parse_args()
+    if args.cmd == "traffic":
+        res = traffic(args.fetch, args.write, args.algorithmic_bytes)
+        if args.workload:
+            res["workload"] = args.workload
+        text = json.dumps(res, indent=1) + "\n"
+        if args.out:
+            args.out.write_text(text)
+        print(text, end="")
+        return 0
+    merged: dict = {}
+    for d in args.dirs:
+        m = means(d)
+        kernel = probed_kernel(m)
+        merged.setdefault(kernel, {}).update({c: v["mean"] for c, v in m[kernel].items()})
+    print(json.dumps(merged, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

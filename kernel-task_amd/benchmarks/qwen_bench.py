@@ -1,6 +1,12 @@
 """The operator on the Qwen3.8-27B layer shapes (bf16, ranks 8 and 16): ours vs the dense GEMM.
 
     python kernel-task_amd/benchmarks/qwen_bench.py --out qwen.json [--tokens 1,8,32,128]
+        [--dtype bfloat16|float16] [--ranks 8,16]
+
+The library carries tuned MFMA tables for these shapes in bf16 at ranks 8 and 16. Other
+dtypes and ranks (fp16; rank 12, which runs the rank-16 kernels on zero-padded links) get
+the variant modules built at prepare time (factorized_inference/jit.py; TRK_JIT=0 runs the
+generic kernel instead, for comparison). Each row records which kind of plan served it.
 
 Role of the reference's tools/qwen_bench.py (shapes from tools/qwen_shapes.py:20-27, bf16,
 seed 0, harness protocol): per shape, rank and token count, the HIP-event stream latency of
@@ -65,22 +71,32 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--out", type=Path, required=True)
     ap.add_argument("--tokens", default="1,8,32,128")
+    ap.add_argument("--dtype", default="bfloat16", choices=("bfloat16", "float16"))
+    ap.add_argument("--ranks", default="8,16")
     args = ap.parse_args()
+    dtype = getattr(torch, args.dtype)
+    ranks = [int(r) for r in args.ranks.split(",")]
     if not torch.cuda.is_available():
         print("qwen_bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     tokens = [int(t) for t in args.tokens.split(",")]
     torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
+    torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
     rows = []
+    shapes = [tilegen.ShapeDecl(f"qwen_{name}", ins, outs, rank)
+              for name, (ins, outs) in tilegen.QWEN.items() for rank in ranks]
     with torch.inference_mode():
-        for shape in (s for s in tilegen.DECLARED if s.name.startswith("qwen_")):
+        for shape in shapes:
             spec = TRSpec(shape.ins, shape.outs, shape.rank)
-            cores = make_cores(spec, device="cuda", dtype=torch.bfloat16, seed=0)
+            cores = make_cores(spec, device="cuda", dtype=dtype, seed=0)
+            t0 = time.perf_counter()
             run = prepare_optimized(cores, spec)
+            torch.cuda.synchronize()
+            prepare_ms = (time.perf_counter() - t0) * 1e3
             w = materialize_dense_weight(cores, spec)
             w64 = materialize_dense_weight([c.double() for c in cores], spec)
             for T in tokens:
-                x = torch.randn(T, spec.in_features, device="cuda", dtype=torch.bfloat16,
+                x = torch.randn(T, spec.in_features, device="cuda", dtype=dtype,
                                 generator=torch.Generator(device="cuda").manual_seed(T))
                 ours = lambda: run(x)  # noqa: E731
                 dense = lambda: dense_forward(x, w)  # noqa: E731
@@ -90,6 +106,9 @@ def main() -> int:
                 ref = sub.double() @ w64.T
                 info = run.selected(T)
                 row = {"shape": shape.name, "key": shape.key, "rank": shape.rank, "tokens": T,
+                       "dtype": args.dtype, "kernel_rank": run.plan.kernel_rank,
+                       "modules": run.plan.modules, "kind": info["kind"],
+                       "prepare_ms": prepare_ms,
                        "in_features": spec.in_features, "out_features": spec.out_features,
                        "variant": info["name"], "ours_us": ours_us, "dense_us": dense_us,
                        "dense_over_ours": dense_us / ours_us,
@@ -106,7 +125,8 @@ def main() -> int:
             del run, w, w64
             torch.cuda.empty_cache()
     args.out.parent.mkdir(parents=True, exist_ok=True)
-    args.out.write_text(json.dumps({"device": torch.cuda.get_device_name(0), "rows": rows},
+    args.out.write_text(json.dumps({"device": torch.cuda.get_device_name(0),
+                                    "trk_jit": os.environ.get("TRK_JIT", "1"), "rows": rows},
                                    indent=1) + "\n")
     print(f"wrote {args.out}", flush=True)
     return 0

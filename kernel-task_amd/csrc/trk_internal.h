@@ -63,6 +63,7 @@ struct Variant {
     int block;       // threads per workgroup
     int lds_bytes;   // dynamic LDS per workgroup
     int t_min, t_max;
+    int xcd_local;   // 1: the launch's work runs on XCD 0 only (KCfg::XL; grid x 8)
     char name[64];
     LaunchFn launch;
 };

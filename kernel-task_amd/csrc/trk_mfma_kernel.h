@@ -125,6 +125,11 @@ struct KCfg {
                              // consecutive steps share one barrier interval; 0: one buffer
     int S1;                  // WIDE stage 1: row tiles per wave (the waves split the columns
                              // NW * S1 / M1T ways); 0: the default split (below)
+    int XL;                  // 1: XCD-local launch. The grid is 8x larger and the dispatcher
+                             // deals workgroups to the 8 XCDs round-robin; those dealt to XCDs
+                             // 1-7 exit at once, so every working workgroup shares XCD 0's L2:
+                             // each core slice crosses from HBM once and every cache line of y
+                             // is written back by one L2 (fewer CUs, for small launches)
 };
 
 // K orders of the packed second- and last-core sections a variant reads (its chain's layout):
@@ -328,6 +333,7 @@ struct Geo {
 
     static_assert(R % 8 == 0 && (R & (R - 1)) == 0, "MFMA variants need a power-of-two rank >= 8");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
+    static_assert(C.XL == 0 || C.XL == 1, "XL is 0 or 1");
     static_assert(C.WIDE >= 0 && C.WIDE <= NW && (C.WIDE == 0 || NW % C.WIDE == 0),
                   "WIDE is 0 or divides the waves");
     static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
@@ -748,9 +754,16 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     const int lrow = lane & 15, lgrp = lane >> 4;
 
     // Workgroups are dealt round-robin to the 8 XCDs, each with its own L2. Renumber them so
-    // that consecutive tiles (same first-core digit f, hence the same Fs slice) share an XCD.
+    // that consecutive tiles (same first-core digit f, hence the same Fs slice) share an XCD;
+    // an XCD-local launch keeps only the workgroups dealt to XCD 0 (blockIdx.x % 8 == 0: with
+    // 8 * NBLK columns the linear workgroup index has the same residue modulo 8).
     int b = blockIdx.x;
-    if constexpr (G::NBLK % 8 == 0) b = (b % 8) * (G::NBLK / 8) + b / 8;
+    if constexpr (C.XL) {
+        if (b % 8 != 0) return;  // uniform per workgroup, before any barrier or access
+        b /= 8;
+    } else if constexpr (G::NBLK % 8 == 0) {
+        b = (b % 8) * (G::NBLK / 8) + b / 8;
+    }
     const int l0 = (b % G::NLC) * G::LC;
     b /= G::NLC;
     const int s0 = (b % G::NSC) * G::SC;
@@ -1220,7 +1233,7 @@ int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const vo
     const size_t aux_elem = (epi.mode & kAuxF32) ? 4 : sizeof(E);
     for (int t0 = 0; t0 < tokens; t0 += per_launch) {
         const int n = tokens - t0 < per_launch ? tokens - t0 : per_launch;
-        const dim3 grid(G::NFC * G::NSC * G::NLC, (n + G::TT - 1) / G::TT);
+        const dim3 grid(G::NFC * G::NSC * G::NLC * (C.XL ? 8 : 1), (n + G::TT - 1) / G::TT);
         const E *xe = static_cast<const E *>(x) + size_t(t0) * G::IN;
         void *yc = static_cast<char *>(y) + size_t(t0) * G::OUT * y_elem;
         const void *ac =
@@ -1249,9 +1262,10 @@ struct Shape {
     int dt, F, S, L, i0, i1, i2, o0, o1, o2, R;
 };
 constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
-                    int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0, int S1 = 0) {
+                    int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0, int S1 = 0,
+                    int XL = 0) {
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
-                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1};
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL};
 }
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>},
@@ -1283,17 +1297,19 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
         v.t_min = e.t_min;
         v.t_max = e.t_max;
         v.launch = e.launch;
+        v.xcd_local = k.XL;
         if (k.WIDE) {
             char s1[8] = "";
             if (k.S1) std::snprintf(s1, sizeof(s1), "_s%d", k.S1);
             std::snprintf(v.name, sizeof(v.name),
-                          "ring3_mfma_wide%d%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
+                          "ring3_mfma_wide%d%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
                           k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "",
-                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, k.F,
+                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, k.XL ? "_xl" : "", k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         } else {
-            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
-                          k.NW == 8 ? "_w8" : "", k.PIPE == 2 ? "_p2" : k.PIPE ? "_p" : "", k.F,
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+                          k.NW == 8 ? "_w8" : "", k.PIPE == 2 ? "_p2" : k.PIPE ? "_p" : "",
+                          k.XL ? "_xl" : "", k.F,
                           k.S, k.L, k.TT, k.FC,
                           k.SC, k.LC, k.IC, k.KS3, k.NACC);
         }

@@ -79,7 +79,7 @@ def module_path(shape: tilegen.ShapeDecl) -> Path | None:
 
 def build_module(shape: tilegen.ShapeDecl, verbose: bool = False) -> Path | None:
     """The path of the compiled module of `shape`, compiling it if needed (one process at a
-    time per cache directory; others wait and reuse it). None when the shape has no tiles."""
+    time per module; others wait and reuse it). None when the shape has no tiles."""
     src = module_source(shape)
     if src is None:
         return None
@@ -87,7 +87,7 @@ def build_module(shape: tilegen.ShapeDecl, verbose: bool = False) -> Path | None
     if path.exists():
         return path
     CACHE.mkdir(parents=True, exist_ok=True)
-    with open(CACHE / ".lock", "w") as lock:
+    with open(path.with_suffix(".lock"), "w") as lock:
         fcntl.flock(lock, fcntl.LOCK_EX)
         if path.exists():
             return path

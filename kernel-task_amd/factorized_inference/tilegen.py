@@ -93,16 +93,19 @@ class Tile:
     PIPE: int = 0  # 1: double-buffered slices, two barriers per step; 2: also double-buffered
     #                stage results, three steps' stages in one barrier interval
     S1: int = 0    # WIDE stage-1 row tiles per wave (0: the kernel's default split)
+    XL: int = 0    # 1: XCD-local launch (all work on XCD 0, one L2; KCfg::XL)
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
         a = [self.TT, self.FC, self.SC, self.LC, self.IC, self.KS3, self.NACC]
-        if (self.WIDE, self.MF2, self.NW, self.PIPE) != (0, 16, 4, 0):
+        if (self.WIDE, self.MF2, self.NW, self.PIPE, self.XL) != (0, 16, 4, 0, 0):
             a += [self.WIDE, self.MF2, self.NW]
-        if self.PIPE or self.S1:
+        if self.PIPE or self.S1 or self.XL:
             a.append(self.PIPE)
-        if self.S1:
+        if self.S1 or self.XL:
             a.append(self.S1)
+        if self.XL:
+            a.append(self.XL)
         return ", ".join(map(str, a))
 
 
@@ -334,6 +337,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (c.nL % t.IC == 0, "IC must divide the last core's input mode"),
         (t.PIPE in (0, 1, 2) and (t.PIPE == 0 or c.nL // t.IC > 1), "a pipelined tile needs two steps"),
         (t.S1 == 0 or (wide and WM1 > 0 and NW % WM1 == 0), "S1 must split the stage-1 rows"),
+        (t.XL in (0, 1), "XL is 0 or 1"),
         (c.xrow or c.IN % 8 == 0, "scatter loader reads x rows in 8-element vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= N2R * P2 * 2, "stage-3 reduction does not fit in Ub"),
@@ -414,6 +418,13 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
         if t is not None and t not in out.values():
             out[f"wide{wide}x32" + ("w8" if nw == 8 else "")] = t
     if extended:
+        # XCD-local single-token tiles (every workgroup on one XCD: one L2 fetches each core
+        # slice once and owns every line of y). Few workgroups read the replicated last-core
+        # slice through that one L2, so each owns all or half of the second core's outputs.
+        for sc, tag in ((c.oS, "all"), (half, "half")):
+            add(f"t1_{tag}_xl", lambda ic, sc=sc: Tile(1, 1, sc, LC, ic, 4, 1, XL=1), small_ics)
+            add(f"t1_{tag}_w8_xl", lambda ic, sc=sc: Tile(1, 1, sc, LC, ic, 4, 1, 0, 16, 8, XL=1),
+                small_ics)
         add("t1_s1_icall", lambda ic: Tile(1, 1, 1, LC, ic, 4, 1), ics)
         add("t1_s2_icall", lambda ic: Tile(1, 1, min(2, c.oS), LC, ic, 4, 1), ics)
         # stage 3 on fewer waves with independent accumulator chains: no cross-wave
@@ -476,7 +487,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
 
 
 _VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?(?:_s(\d+))?|(_w8)?(_p2?)?)"
-                           r"<(\d)(\d)(\d),"
+                           r"(_xl)?<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -486,12 +497,13 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     if not m:
         raise ValueError(f"not an MFMA variant name: {name!r}")
     wide = int(m.group(1) or 0)
-    order = tuple(int(m.group(i)) for i in (8, 9, 10))
-    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(11, 18))
+    order = tuple(int(m.group(i)) for i in (9, 10, 11))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(12, 19))
     pipe_tag = m.group(4) or m.group(7) or ""
     pipe = 2 if pipe_tag.endswith("2") else 1 if pipe_tag else 0
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
-                       8 if (m.group(3) or m.group(6)) else 4, pipe, int(m.group(5) or 0))
+                       8 if (m.group(3) or m.group(6)) else 4, pipe, int(m.group(5) or 0),
+                       1 if m.group(8) else 0)
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
@@ -553,12 +565,16 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
           extended: bool = False) -> list[tuple[str, tuple, Tile, int, int]]:
     """[(name, order, tile, t_min, t_max)] for one shape: the tuned winners when the shape
     has measurements, else every candidate with the rule's ranges (0, 0: index only).
+    A tuned entry's "extra" tiles are compiled index-only beside the winners (alternatives
+    a caller may route token counts to, such as the XCD-local tiles).
     all_candidates=True ignores the measurements (the autotuner's input)."""
     tuned = load_tuned() if tuned is None else tuned
     entry = None if all_candidates else tuned.get(shape.key)
     if entry:
         rows = [(r["name"], tuple(r.get("order", entry["order"])), Tile(**r["tile"]),
                  r["t_min"], r["t_max"]) for r in entry["ranges"]]
+        rows += [(r["name"], tuple(r.get("order", entry["order"])), Tile(**r["tile"]), 0, 0)
+                 for r in entry.get("extra", [])]
         for name, order, t, _, _ in rows:
             why = geometry(shape, order, t)["reject"]
             if why:
@@ -571,7 +587,7 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
         # the previous winners stay candidates, so a new search never loses a tile it had;
         # an extended search also tries their larger stage-1 row groups (a local refinement)
         entry = tuned[shape.key]
-        for r in entry["ranges"]:
+        for r in entry["ranges"] + entry.get("extra", []):
             order = tuple(r.get("order", entry["order"]))
             if order not in ORDERS:
                 continue

@@ -246,6 +246,32 @@ def test_every_variant(shape, rank, dtype):
             check_result(y, oracle_y(x, cores, spec), dtype)
 
 
+# ---- the XCD-local route (PreparedTRKernel.use_xcd_local) ------------------------------------
+def test_xcd_local_route():
+    announce(test="xcd_local", rank=8)
+    spec = TRSpec(rank=8, **DEFAULT)
+    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=5)
+    run = prepare_optimized(cores, spec)
+    default = run.selected(1)
+    assert run.use_xcd_local()
+    info = run.selected(1)
+    assert "_xl<" in info["name"] and "_xl<" not in default["name"]
+    # every workgroup of an XCD-local grid that is not dealt to XCD 0 exits: 8x the columns
+    tile = info["tile"]
+    assert info["grid"][0] == 8 * (24 // tile[1]) * (10 // tile[2]) * (12 // tile[3])
+    assert "_xl<" not in run.selected(2)["name"]
+    for tokens in (1, 2, 1):
+        x = gpu_x(spec, tokens, 60 + tokens, torch.float16)
+        y = run(x)
+        torch.cuda.synchronize()
+        check_result(y, oracle_y(x, cores, spec), torch.float16)
+    # a plan without an XCD-local variant keeps its routing
+    spec16 = TRSpec(rank=16, **DEFAULT)
+    run16 = prepare_optimized(make_cores(spec16, device="cuda", dtype=torch.float16, seed=5), spec16)
+    before = run16.selected(1)["name"]
+    assert not run16.use_xcd_local() and run16.selected(1)["name"] == before
+
+
 # ---- odd shapes and fp32 (tools/check_kernel.py:63-101, check_bf16.py) ---------------------
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("ins,outs,rank", [

@@ -45,8 +45,29 @@ def test_variant_names_parse_back_to_their_tiles():
     assert parse("ring3_mfma_p2<210,1,1,10,12,2,1,2>")[1].PIPE == 2
     assert parse("ring3_mfma_wide8x32w8p2<210,2,1,16,16,1,1,2>")[1] == tilegen.Tile(
         2, 1, 16, 16, 1, 1, 2, 8, 32, 8, 2)
+    assert parse("ring3_mfma_w8_xl<210,1,1,10,12,8,4,1>")[1] == tilegen.Tile(
+        1, 1, 10, 12, 8, 4, 1, 0, 16, 8, XL=1)
+    assert parse("ring3_mfma_wide8x32w8p_s4_xl<210,4,1,10,12,2,2,1>")[1] == tilegen.Tile(
+        4, 1, 10, 12, 2, 2, 1, 8, 32, 8, 1, 4, 1)
     with pytest.raises(ValueError):
         parse("ring3_generic<012,rc=8>")
+
+
+def test_xcd_local_tiles_emit_every_trailing_argument():
+    # XL is the last argument of tile(shape, ...), so an XCD-local tile spells out the
+    # defaults before it
+    assert tilegen.Tile(1, 1, 10, 12, 8, 4, 1, 0, 16, 8, XL=1).args() == \
+        "1, 1, 10, 12, 8, 4, 1, 0, 16, 8, 0, 0, 1"
+    assert tilegen.Tile(1, 1, 2, 12, 8, 4, 1).args() == "1, 1, 2, 12, 8, 4, 1"
+    # the headline shape's table carries an XCD-local tile, index-only, beside its winners
+    shape = tilegen.BASELINE[0]
+    xl = [(n, t, lo, hi) for n, _, t, lo, hi in tilegen.table(shape) if t.XL]
+    assert xl and all((lo, hi) == (0, 0) for *_, lo, hi in xl)
+    # and the extended search offers XCD-local single-token tiles
+    assert any(t.XL for t in tilegen.candidates(shape, extended=True).values())
+    plan = _lib.Plan(shape.ins, shape.outs, shape.rank, DT[shape.dtype])
+    v = next(v for v in plan.variants(1) if "_xl<" in v["name"])
+    assert v["grid"][0] == 8 * 24 and v["t_min"] == 0
 
 
 @pytest.mark.parametrize("shape", HAND + tilegen.DECLARED, ids=lambda s: s.key)
