@@ -1,9 +1,12 @@
-"""Summaries of `rocprofv3 --pmc ... -f csv` runs of `bench.py --traffic-probe`.
+"""Summaries of rocprofv3 csv output: `--pmc` runs of `bench.py --traffic-probe`, and
+kernel traces.
 
     # HBM traffic per launch (one FETCH_SIZE run and one WRITE_SIZE run of the same probe)
     python kernel-task_amd/benchmarks/counters.py traffic --fetch DIR --write DIR --out FILE.json
     # per-dispatch means of every counter of the probed kernel, one or more runs
     python kernel-task_amd/benchmarks/counters.py means DIR [DIR ...]
+    # back-to-back blocks of one kernel in a --kernel-trace run (e.g. bench.py's timed block)
+    python kernel-task_amd/benchmarks/counters.py blocks TRACE.csv --kernel REGEX [--grid N]
 
 A probe run (bench.py --traffic-probe CALLS) launches one tensor-ring kernel CALLS times and
 then copies a 512 MiB buffer 5 times. The copy is larger than every L2 and the 256 MB MALL,
@@ -90,6 +93,37 @@ def traffic(fetch_dir: Path, write_dir: Path, algorithmic_bytes: float | None) -
     return out
 
 
+def blocks(trace: Path, pattern: str, grid: int | None = None, max_gap_us: float = 30.0,
+           min_len: int = 10) -> list[dict]:
+    """Runs of consecutive dispatches of the kernels matching `pattern` (and grid size
+    `grid`, in threads) whose gaps from the previous dispatch's end stay under max_gap_us:
+    bench.py's timed blocks, told apart from isolated calls. Per run: dispatches, mean and
+    min duration, first start (us from the first dispatch)."""
+    with open(trace, newline="") as f:
+        rows = [r for r in csv.DictReader(f) if re.search(pattern, r["Kernel_Name"]) and
+                (grid is None or int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) == grid)]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    if not rows:
+        return []
+    t0 = int(rows[0]["Start_Timestamp"])
+    runs, cur, prev_end = [], [], None
+    for r in rows:
+        s, e = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if prev_end is not None and (s - prev_end) / 1e3 > max_gap_us:
+            runs.append(cur)
+            cur = []
+        cur.append((s, e))
+        prev_end = e
+    runs.append(cur)
+    out = []
+    for run in runs:
+        if len(run) >= min_len:
+            d = [(e - s) / 1e3 for s, e in run]
+            out.append({"dispatches": len(run), "mean_us": sum(d) / len(d), "min_us": min(d),
+                        "start_us": (run[0][0] - t0) / 1e3})
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -101,7 +135,15 @@ def main() -> int:
     t.add_argument("--out", type=Path)
     mp = sub.add_parser("means")
     mp.add_argument("dirs", type=Path, nargs="+")
+    bp = sub.add_parser("blocks")
+    bp.add_argument("trace", type=Path)
+    bp.add_argument("--kernel", required=True, help="regular expression on the kernel name")
+    bp.add_argument("--grid", type=int, default=None, help="grid size in threads (x * y)")
+    bp.add_argument("--max-gap-us", type=float, default=30.0)
     args = ap.parse_args()
+    if args.cmd == "blocks":
+        print(json.dumps(blocks(args.trace, args.kernel, args.grid, args.max_gap_us), indent=1))
+        return 0
     if args.cmd == "traffic":
         res = traffic(args.fetch, args.write, args.algorithmic_bytes)
         if args.workload:

@@ -65,7 +65,10 @@ def _fingerprint(src: str) -> str:
     for name in HEADERS:
         h.update((build_ext.CSRC / name).read_bytes())
     h.update((build_ext.INCLUDE / "trk.h").read_bytes())
-    h.update(" ".join(build_ext.HIPCC_FLAGS).encode())
+    # the flags without the include directories: those are absolute paths of this checkout,
+    # and the headers they point to are hashed above, so a copy of the tree elsewhere (a
+    # GPU box) reuses the modules built here
+    h.update(" ".join(f for f in build_ext.HIPCC_FLAGS if not f.startswith("-I")).encode())
     return h.hexdigest()[:16]
 
 

@@ -55,6 +55,19 @@ def test_undeclared_shapes_get_mfma_variants(ins, outs, rank, dtype):
     assert plan.describe(-1, 1)["bytes"] == 2.0 * (params + spec.in_features + spec.out_features)
 
 
+def test_module_names_do_not_depend_on_the_checkout_path(monkeypatch):
+    # the tree is copied to other paths (a GPU box): modules built here must keep their names
+    from factorized_inference import build_ext
+    shape = tilegen.ShapeDecl("prepared", (4, 6, 8), (6, 4, 8), 8, "f16")
+    here = jit.module_path(shape)
+    moved = [f"-I/elsewhere/{f[2:].lstrip('/')}" if f.startswith("-I") else f
+             for f in build_ext.HIPCC_FLAGS]
+    monkeypatch.setattr(build_ext, "HIPCC_FLAGS", moved)
+    assert jit.module_path(shape) == here
+    monkeypatch.setattr(build_ext, "HIPCC_FLAGS", moved + ["-O2"])
+    assert jit.module_path(shape) != here
+
+
 def test_fp32_and_disabled_jit_keep_the_generic_kernel(monkeypatch):
     spec = TRSpec((4, 6, 8), (6, 4, 8), 8)
     assert not make_plan(spec, torch.float32).has_mfma
