@@ -1,0 +1,357 @@
+// Persistent multi-layer stack of tensor-ring layers: L layers in one launch, alternating
+// 1920->2880 and 2880->1920 (rank STACK_RANK, fp16), a grid-wide barrier between layers.
+// Built by kernel-task_amd/benchmarks/stack_bench.py; prints one JSON object per (variant, L).
+//
+// Role of the reference's weight-stationary stack experiment (kernel_work/stack/tr_stack.cu:1-40,
+// kernel-design/WEIGHT_STATIONARY.md:104-147): does one persistent kernel beat the same
+// layers launched one by one? Own design on the MI355X kernel: every unit of a layer is one
+// call of ring3_unit (the standalone kernel's body), each output owned by one workgroup, so
+// there are no atomics on activations and the result is bitwise that of per-layer launches
+// (checked here for every L). Two forms:
+//   STACK_XCD 0  workgroups on every XCD; between layers a device-scope barrier (release:
+//                write the L2 back; acquire: invalidate it), the only portable form
+//   STACK_XCD 1  workgroups on one XCD (a grid of 8x the working workgroups, those dealt to
+//                XCDs 1-7 exit at once): all of the stack shares one L2, so a barrier is an
+//                atomic in that L2 plus an L1 invalidation; split into arrive (after a layer)
+//                and wait (inside the next layer's first unit, once its core-slice loads are
+//                in flight, which do not depend on the activations)
+// Every barrier wait is bounded (it sets an error flag and gives up), and the launch is
+// cooperative, so the runtime refuses a grid whose workgroups could not all be resident.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "trk.h"
+#include "trk_mfma_kernel.h"
+
+using namespace trk;
+
+#define CHECK(x)                                                                              \
+    do {                                                                                      \
+        auto e_ = (x);                                                                        \
+        if (e_) {                                                                             \
+            std::fprintf(stderr, "%s failed (%d) at line %d\n", #x, int(e_), __LINE__);       \
+            std::exit(1);                                                                     \
+        }                                                                                     \
+    } while (0)
+
+#ifndef STACK_RANK
+#define STACK_RANK 8
+#endif
+#ifndef STACK_XCD
+#define STACK_XCD 0
+#endif
+
+// layer shapes and their chain orders (the least padded MFMA work of each)
+constexpr Shape kUp{TRK_DTYPE_F16, 2, 1, 0, 8, 12, 20, 12, 10, 24, STACK_RANK};
+constexpr Shape kDown{TRK_DTYPE_F16, 2, 0, 1, 12, 10, 24, 8, 12, 20, STACK_RANK};
+// tokens=1 tiles: every XCD, the tuned single-token tiles (4 waves); one XCD, tiles that own
+// all second-core outputs (8 waves), so that 24 and 20 units fill most of its 32 CUs
+#if STACK_XCD
+constexpr KCfg CU = tile(kUp, 1, 1, 10, 12, 8, 4, 1, 0, 16, 8);
+constexpr KCfg CD = tile(kDown, 1, 1, 8, 12, 10, 4, 1, 0, 16, 8);
+#else
+constexpr KCfg CU = tile(kUp, 1, 1, 2, 12, 8, 4, 1);
+constexpr KCfg CD = tile(kDown, 1, 1, 2, 12, 10, 4, 1);
+#endif
+using GU = Geo<CU>;
+using GD = Geo<CD>;
+static_assert(GU::NT == GD::NT, "both layer tiles need the same workgroup size");
+constexpr int NT = GU::NT;
+constexpr int POOL = GU::LDS_ELEMS > GD::LDS_ELEMS ? GU::LDS_ELEMS : GD::LDS_ELEMS;
+constexpr int NWG = GU::NBLK > GD::NBLK ? GU::NBLK : GD::NBLK;  // working workgroups
+using E = typename Ops<CU.dt>::E;
+
+struct Layer {
+    const E *fk, *sk, *lk;
+};
+
+// device-scope barrier: every workgroup's stores written back from its L2 before it arrives,
+// the L2 invalidated after the wait (the compiler's release/acquire at agent scope)
+__device__ __forceinline__ void device_barrier(unsigned *counter, unsigned target, int *err,
+                                               int spin) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        for (int n = 0; __hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) <
+                        target;) {
+            if (++n > spin) {
+                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+}
+
+// one-XCD barrier, arrive half: this workgroup's stores have reached the shared L2, then one
+// atomic in that L2 (workgroup scope: no writeback)
+__device__ __forceinline__ void xcd_arrive(unsigned *counter) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// one-XCD barrier, wait half. The counter is read with compare-and-swaps that never swap (it
+// never holds 2^32 - 1): they execute in the L2 and return its value, while a plain load may
+// be served a stale L1 line (and the compiler turns an atomic add of 0 into such a load).
+// Then the CU's L1 is invalidated, so the next reads of activations come from the L2.
+__device__ __forceinline__ void xcd_wait(unsigned *counter, unsigned target, int *err, int spin) {
+    if (threadIdx.x == 0) {
+        for (int n = 0;;) {
+            unsigned v = 0xffffffffu;
+            __hip_atomic_compare_exchange_strong(counter, &v, 0xffffffffu, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (v >= target) break;
+            if (++n > spin) {
+                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+    asm volatile("buffer_inv sc0" ::: "memory");
+}
+
+// This workgroup's units of one layer. A nonzero target means the previous layer's barrier is
+// still open: with PREFETCH the first unit waits inside ring3_unit once its core-slice loads
+// are in flight; without, before it starts; a workgroup without a unit waits at the end.
+template <KCfg C, bool PREFETCH>
+__device__ __forceinline__ void run_layer(const Layer &lay, const E *in, E *out, int T, int wg,
+                                          E *pool, unsigned *counter, unsigned target, int *err,
+                                          int spin) {
+    using G = Geo<C>;
+    const int units = G::NBLK * ((T + G::TT - 1) / G::TT);
+    bool pending = target != 0;
+    for (int u = wg; u < units; u += NWG) {
+        auto wait = [&]() {
+            if (pending) xcd_wait(counter, target, err, spin);
+            pending = false;
+        };
+        if constexpr (PREFETCH) {
+            ring3_unit<C, false>(in, lay.fk, lay.sk, lay.lk, out, T, 0, nullptr, u % G::NBLK,
+                                 u / G::NBLK, pool + G::oFs, pool + G::oSs, pool + G::oLs,
+                                 pool + G::oXs, pool + G::oUb, pool + G::oVb, wait);
+        } else {
+            wait();
+            ring3_unit<C, false>(in, lay.fk, lay.sk, lay.lk, out, T, 0, nullptr, u % G::NBLK,
+                                 u / G::NBLK, pool + G::oFs, pool + G::oSs, pool + G::oLs,
+                                 pool + G::oXs, pool + G::oUb, pool + G::oVb);
+        }
+        __syncthreads();  // the next unit reuses the LDS
+    }
+    if (pending) xcd_wait(counter, target, err, spin);
+}
+
+// WORK false: the barriers alone. Layer l reads x (l = 0) or act[(l-1) & 1] and writes y
+// (l = L-1) or act[l & 1]. The counter only grows: launch k waits for base + l * NWG.
+template <bool WORK, bool PREFETCH>
+__global__ void __launch_bounds__(NT)
+    stack_kernel(const E *x, E *act0, E *act1, E *y, const Layer *layers, int L, int T,
+                 unsigned *counter, unsigned base, int *err, int spin) {
+    __shared__ __attribute__((aligned(16))) E pool[POOL];
+    int wg = blockIdx.x;
+    if constexpr (STACK_XCD) {
+        if (wg % 8 != 0) return;  // dealt to XCDs 1-7
+        wg /= 8;
+    }
+    for (int l = 0; l < L; ++l) {
+        const E *in = l == 0 ? x : ((l - 1) & 1 ? act1 : act0);
+        E *out = l == L - 1 ? y : (l & 1 ? act1 : act0);
+        if constexpr (STACK_XCD) {
+            const unsigned target = l > 0 ? base + unsigned(l) * NWG : 0u;
+            if constexpr (WORK) {
+                if (l % 2 == 0)
+                    run_layer<CU, PREFETCH>(layers[l], in, out, T, wg, pool, counter, target, err, spin);
+                else
+                    run_layer<CD, PREFETCH>(layers[l], in, out, T, wg, pool, counter, target, err, spin);
+            } else if (target) {
+                xcd_wait(counter, target, err, spin);
+            }
+            if (l + 1 < L) xcd_arrive(counter);
+        } else {
+            if constexpr (WORK) {
+                if (l % 2 == 0)
+                    run_layer<CU, false>(layers[l], in, out, T, wg, pool, counter, 0u, err, spin);
+                else
+                    run_layer<CD, false>(layers[l], in, out, T, wg, pool, counter, 0u, err, spin);
+            }
+            if (l + 1 < L) device_barrier(counter, base + unsigned(l + 1) * NWG, err, spin);
+        }
+    }
+}
+
+int main(int argc, char **argv) {
+    std::setvbuf(stdout, nullptr, _IOLBF, 0);
+    const int T = argc > 1 ? std::atoi(argv[1]) : 1;
+    std::vector<int> Ls;
+    for (int a = 2; a < argc; ++a) Ls.push_back(std::atoi(argv[a]));
+    if (Ls.empty()) Ls = {8, 32, 128};
+    if (T < 1 || T > 64 || *std::min_element(Ls.begin(), Ls.end()) < 1) {
+        std::fprintf(stderr, "usage: stack_bench T(1..64) L [L ...]\n");
+        return 2;
+    }
+    const int Lmax = *std::max_element(Ls.begin(), Ls.end());
+    const int R = STACK_RANK;
+    const int m_up[3] = {8, 12, 20}, m_down[3] = {12, 10, 24};
+    trk_plan *pu, *pd;
+    CHECK(trk_plan_create(m_up, m_down, R, TRK_DTYPE_F16, &pu));
+    CHECK(trk_plan_create(m_down, m_up, R, TRK_DTYPE_F16, &pd));
+    const int ou[3] = {CU.F, CU.S, CU.L}, od[3] = {CD.F, CD.S, CD.L};
+    Plan *PU = reinterpret_cast<Plan *>(pu), *PD = reinterpret_cast<Plan *>(pd);
+    const int cu = plan_chain(PU, ou, s_group(CU), l_group(CU), s_frag(CU));
+    const int cd = plan_chain(PD, od, s_group(CD), l_group(CD), s_frag(CD));
+    if (cu < 0 || cd < 0) {
+        std::fprintf(stderr, "no packed chain for the stack's tiles\n");
+        return 1;
+    }
+    std::mt19937 rng(7);
+    std::normal_distribution<float> nd(0.f, 1.f);
+    // distinct cores per layer, per-core sigma (make_cores) so activations stay O(1)
+    std::vector<void *> owned;
+    auto make_layer = [&](trk_plan *p, const int *in, const int *out, int chain) {
+        const double sig = std::pow(double(in[0] * in[1] * in[2]) * R * R * R, -1.0 / 6.0);
+        void *g[3];
+        for (int k = 0; k < 3; ++k) {
+            const size_t n = size_t(R) * out[k] * in[k] * R;
+            std::vector<E> h(n);
+            for (auto &v : h) v = E(float(nd(rng) * sig));
+            CHECK(hipMalloc(&g[k], n * sizeof(E)));
+            CHECK(hipMemcpy(g[k], h.data(), n * sizeof(E), hipMemcpyHostToDevice));
+        }
+        char *packed;
+        CHECK(hipMalloc(&packed, trk_plan_packed_bytes(p)));
+        owned.push_back(packed);
+        CHECK(trk_pack(p, g[0], g[1], g[2], packed, nullptr));
+        CHECK(hipDeviceSynchronize());
+        for (int k = 0; k < 3; ++k) CHECK(hipFree(g[k]));
+        const Chain &c = reinterpret_cast<Plan *>(p)->chains[chain];
+        return Layer{reinterpret_cast<const E *>(packed + c.offF),
+                     reinterpret_cast<const E *>(packed + c.offS),
+                     reinterpret_cast<const E *>(packed + c.offL)};
+    };
+    std::vector<Layer> layers;
+    for (int l = 0; l < Lmax; ++l)
+        layers.push_back(l % 2 == 0 ? make_layer(pu, m_up, m_down, cu) : make_layer(pd, m_down, m_up, cd));
+    Layer *dlayers;
+    CHECK(hipMalloc(&dlayers, sizeof(Layer) * Lmax));
+    CHECK(hipMemcpy(dlayers, layers.data(), sizeof(Layer) * Lmax, hipMemcpyHostToDevice));
+    constexpr int MAXF = 2880;  // widest activation row
+    std::vector<E> hx(size_t(T) * 1920);
+    for (auto &v : hx) v = E(nd(rng));
+    E *x, *a0, *a1, *y, *yr, *b0, *b1;
+    CHECK(hipMalloc(&x, hx.size() * sizeof(E)));
+    CHECK(hipMemcpy(x, hx.data(), hx.size() * sizeof(E), hipMemcpyHostToDevice));
+    for (E **p : {&a0, &a1, &y, &yr, &b0, &b1}) CHECK(hipMalloc(p, size_t(T) * MAXF * sizeof(E)));
+    unsigned *counter;
+    int *err;
+    CHECK(hipMalloc(&counter, sizeof(unsigned)));
+    CHECK(hipMalloc(&err, sizeof(int)));
+    CHECK(hipMemset(counter, 0, sizeof(unsigned)));
+    CHECK(hipMemset(err, 0, sizeof(int)));
+    const int grid = STACK_XCD ? 8 * NWG : NWG;
+    const int spin = 1 << 14;  // polls of ~27 ns: ~0.4 ms before a barrier gives up
+    unsigned base = 0;
+
+    auto per_layer = [&](int L, hipStream_t s) {  // the same tiles, one standalone launch each
+        for (int l = 0; l < L; ++l) {
+            const E *in = l == 0 ? x : ((l - 1) & 1 ? b1 : b0);
+            E *out = l == L - 1 ? yr : (l & 1 ? b1 : b0);
+            if (l % 2 == 0)
+                hipLaunchKernelGGL((ring3_mfma_kernel<CU, false>), dim3(GU::NBLK, (T + GU::TT - 1) / GU::TT),
+                                   dim3(NT), 0, s, in, layers[l].fk, layers[l].sk, layers[l].lk,
+                                   (void *)out, T, 0, (const void *)nullptr);
+            else
+                hipLaunchKernelGGL((ring3_mfma_kernel<CD, false>), dim3(GD::NBLK, (T + GD::TT - 1) / GD::TT),
+                                   dim3(NT), 0, s, in, layers[l].fk, layers[l].sk, layers[l].lk,
+                                   (void *)out, T, 0, (const void *)nullptr);
+        }
+    };
+    auto stack = [&](int L, bool work, bool prefetch) {
+        int Ti = T, Li = L, spini = spin;
+        void *args[] = {&x, &a0, &a1, &y, &dlayers, &Li, &Ti, &counter, &base, &err, &spini};
+        const void *fn = work ? (prefetch ? (const void *)stack_kernel<true, true>
+                                          : (const void *)stack_kernel<true, false>)
+                              : (const void *)stack_kernel<false, false>;
+        CHECK(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(NT), args, 0, nullptr));
+        base += unsigned(L - 1) * NWG;
+    };
+    hipEvent_t e0, e1;
+    CHECK(hipEventCreate(&e0));
+    CHECK(hipEventCreate(&e1));
+    auto time_us = [&](auto &&fn, int reps) {  // median of 5 blocks of back-to-back calls
+        for (int i = 0; i < 3; ++i) fn();
+        CHECK(hipDeviceSynchronize());
+        std::vector<float> t;
+        for (int r = 0; r < 5; ++r) {
+            CHECK(hipEventRecord(e0, nullptr));
+            for (int i = 0; i < reps; ++i) fn();
+            CHECK(hipEventRecord(e1, nullptr));
+            CHECK(hipEventSynchronize(e1));
+            float ms;
+            CHECK(hipEventElapsedTime(&ms, e0, e1));
+            t.push_back(ms * 1000.f / reps);
+        }
+        std::sort(t.begin(), t.end());
+        return t[2];
+    };
+    const bool prefetch_modes[2] = {false, true};
+    for (int L : Ls) {
+        const int reps = std::max(2, 2000 / L);
+        hipStream_t cs;
+        CHECK(hipStreamCreate(&cs));
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        CHECK(hipStreamBeginCapture(cs, hipStreamCaptureModeGlobal));
+        per_layer(L, cs);
+        CHECK(hipStreamEndCapture(cs, &g));
+        CHECK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        const float t_eager = time_us([&] { per_layer(L, nullptr); }, reps);
+        const float t_graph = time_us([&] { CHECK(hipGraphLaunch(ge, nullptr)); }, reps);
+        const float t_bar = time_us([&] { stack(L, false, false); }, reps);
+        for (int m = 0; m < (STACK_XCD ? 2 : 1); ++m) {
+            const bool pf = prefetch_modes[m];
+            // correctness: bitwise against the per-layer launches of the same tiles
+            CHECK(hipMemset(y, 0xff, size_t(T) * MAXF * sizeof(E)));
+            stack(L, true, pf);
+            per_layer(L, nullptr);
+            CHECK(hipDeviceSynchronize());
+            int herr = 0;
+            CHECK(hipMemcpy(&herr, err, sizeof(int), hipMemcpyDeviceToHost));
+            if (herr) {
+                std::printf("{\"error\": \"a barrier reached its spin bound\", \"L\": %d}\n", L);
+                return 3;
+            }
+            const int outn = (L % 2 == 1 ? 2880 : 1920) * T;
+            std::vector<E> h1(outn), h2(outn);
+            CHECK(hipMemcpy(h1.data(), y, outn * sizeof(E), hipMemcpyDeviceToHost));
+            CHECK(hipMemcpy(h2.data(), yr, outn * sizeof(E), hipMemcpyDeviceToHost));
+            size_t diff = 0;
+            for (int i = 0; i < outn; ++i) diff += std::memcmp(&h1[i], &h2[i], sizeof(E)) != 0;
+            const float t_stack = time_us([&] { stack(L, true, pf); }, reps);
+            CHECK(hipMemcpy(&herr, err, sizeof(int), hipMemcpyDeviceToHost));
+            std::printf("{\"form\": \"%s\", \"prefetch\": %s, \"rank\": %d, \"tokens\": %d, \"layers\": %d, "
+                        "\"workgroups\": %d, \"stack_us\": %.3f, \"barriers_only_us\": %.3f, "
+                        "\"per_layer_eager_us\": %.3f, \"per_layer_graph_us\": %.3f, "
+                        "\"outputs_differing\": %zu, \"outputs\": %d, \"barrier_timeouts\": %d}\n",
+                        STACK_XCD ? "one_xcd" : "all_xcds", pf ? "true" : "false", R, T, L, NWG,
+                        t_stack, t_bar, t_eager, t_graph, diff, outn, herr);
+        }
+        CHECK(hipGraphExecDestroy(ge));
+        CHECK(hipGraphDestroy(g));
+        CHECK(hipStreamDestroy(cs));
+    }
+    for (void *p : owned) CHECK(hipFree(p));
+    trk_plan_destroy(pu);
+    trk_plan_destroy(pd);
+    return 0;
+}

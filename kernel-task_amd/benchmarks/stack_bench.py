@@ -1,0 +1,97 @@
+"""Persistent multi-layer stack: build and run stack_bench.hip in its two forms.
+
+    python kernel-task_amd/benchmarks/stack_bench.py --build            (any machine with hipcc)
+    python kernel-task_amd/benchmarks/stack_bench.py --out stack.json [--tokens 1] [--layers 8,32,128]
+
+Builds kernel-task_amd/benchmarks/_bin/stack_bench_{all,xcd} against libtrk.so (the same
+compiler flags as the library) and, on an MI355X, runs both: every XCD with a device-scope
+barrier, and one XCD with an L2 barrier (with and without prefetching the next layer's core
+slices across it). Each line compares the stack with the same tiles launched once per layer,
+eagerly and in a HIP graph, and checks that the stack's output equals theirs bit for bit.
+
+Role of the reference's stack experiment and its one-GPU measurement plan
+(kernel_work/stack/tr_stack.cu:1-40, kernel-design/WEIGHT_STATIONARY.md:104-147).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent))
+
+from factorized_inference import build_ext  # noqa: E402
+
+SOURCE = HERE / "stack_bench.hip"
+BIN = HERE / "_bin"
+FORMS = {"all": 0, "xcd": 1}
+
+
+def binary(form: str) -> Path:
+    return BIN / f"stack_bench_{form}"
+
+
+def build(verbose: bool = False) -> list[Path]:
+    """Compile both forms (rank 8) into _bin/; raises with hipcc's message on failure."""
+    BIN.mkdir(exist_ok=True)
+    lib = build_ext.PACKAGE
+    out = []
+    for form, xcd in FORMS.items():
+        cmd = [build_ext._hipcc(), *build_ext.HIPCC_FLAGS, f"-DSTACK_XCD={xcd}", "-DSTACK_RANK=8",
+               str(SOURCE), "-o", str(binary(form)), f"-L{lib}", "-l:libtrk.so",
+               f"-Wl,-rpath,{lib}"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        done = subprocess.run(cmd, capture_output=True, text=True)
+        if done.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {SOURCE.name} ({form}):\n{done.stderr[-4000:]}")
+        out.append(binary(form))
+    return out
+
+
+def run(form: str, tokens: int, layers: list[int], timeout: float = 240.0) -> list[dict]:
+    """Run one form; returns its JSON lines. Raises if the program fails or reports an error."""
+    path = binary(form)
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built; run with --build first")
+    done = subprocess.run([str(path), str(tokens), *map(str, layers)], capture_output=True,
+                          text=True, timeout=timeout)
+    rows = [json.loads(ln) for ln in done.stdout.splitlines() if ln.startswith("{")]
+    if done.returncode != 0 or any("error" in r for r in rows):
+        raise RuntimeError(f"{path.name} failed ({done.returncode}):\n{done.stdout}\n{done.stderr}")
+    return rows
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--build", action="store_true", help="compile the two forms and exit")
+    ap.add_argument("--out", type=Path)
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--layers", default="8,32,128")
+    args = ap.parse_args()
+    if args.build:
+        for p in build(verbose=True):
+            print(p)
+        return 0
+    layers = [int(v) for v in args.layers.split(",")]
+    rows = []
+    for form in FORMS:
+        for r in run(form, args.tokens, layers):
+            rows.append(r)
+            print(f"{r['form']:8s} prefetch={str(r['prefetch']):5s} T={r['tokens']} L={r['layers']:4d}: "
+                  f"stack {r['stack_us'] / r['layers']:.3f} us/layer, barriers "
+                  f"{r['barriers_only_us'] / r['layers']:.3f}, per-layer eager "
+                  f"{r['per_layer_eager_us'] / r['layers']:.3f}, graph "
+                  f"{r['per_layer_graph_us'] / r['layers']:.3f}; outputs differing "
+                  f"{r['outputs_differing']} of {r['outputs']}", flush=True)
+    if args.out:
+        args.out.parent.mkdir(parents=True, exist_ok=True)
+        args.out.write_text(json.dumps({"rows": rows}, indent=1) + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -719,56 +719,49 @@ __device__ __forceinline__ void reg_gemm32(const RegA32<O, BMW, K> &A, const typ
     }
 }
 
-// EPI: false compiles the plain store of the plan's dtype only (epi_mode is ignored); true
-// compiles every epilogue, chosen at run time by epi_mode. Two instantiations keep the plain
-// path's code exactly as it is without epilogues (measured: a run-time branch in its store
-// loop cost up to 0.8 us at tokens 8-32).
-template <KCfg C, bool EPI>
-__global__ void __launch_bounds__(Geo<C>::NT)
-    ring3_mfma_kernel(const typename Ops<C.dt>::E *__restrict__ x,
-                      const typename Ops<C.dt>::E *__restrict__ Fk,
-                      const typename Ops<C.dt>::E *__restrict__ Sk,
-                      const typename Ops<C.dt>::E *__restrict__ Lk, void *y, int T,
-                      int epi_mode, const void *aux) {  // aux may equal y
-    // The arguments fill 14 dwords, all of which arrive preloaded in SGPRs
-    // (-amdgpu-kernarg-preload-count): one more would be fetched from the kernel-argument
-    // segment, which lives in host memory when HIP_FORCE_DEV_KERNARG=0, and the first LDS
-    // wait (lgkmcnt also counts scalar loads) would stall on that PCIe read.
+// Hook of ring3_unit for callers without one (the standalone kernel).
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
+// One workgroup's unit of work: the tile b (f, s and l chunks, in the order of NBLK) of token
+// tile tile_y, on the LDS buffers the caller declares (each buffer its own object where the
+// caller can, so that the compiler sees they never alias). Every thread of the workgroup
+// calls it. The standalone kernel below calls it once per workgroup; a persistent caller may
+// call it for several units and layers, with a barrier (__syncthreads) between units.
+// hook, when given, is called by every thread once the unit's core-slice loads are in flight
+// and before any load of x, which is then issued after it: a persistent caller's wait for the
+// layer that writes x (the core slices do not depend on it). Without a hook the loads keep
+// the standalone order.
+template <KCfg C, bool EPI, class Hook = NoHook>
+__device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restrict__ x,
+                                           const typename Ops<C.dt>::E *__restrict__ Fk,
+                                           const typename Ops<C.dt>::E *__restrict__ Sk,
+                                           const typename Ops<C.dt>::E *__restrict__ Lk, void *y,
+                                           int T, int epi_mode, const void *aux, int b, int tile_y,
+                                           typename Ops<C.dt>::E *__restrict__ Fs,
+                                           typename Ops<C.dt>::E *__restrict__ Ss,
+                                           typename Ops<C.dt>::E *__restrict__ Ls,
+                                           typename Ops<C.dt>::E *__restrict__ Xs,
+                                           typename Ops<C.dt>::E *__restrict__ Ub,
+                                           typename Ops<C.dt>::E *__restrict__ Vb,
+                                           Hook &&hook = Hook{}) {
+    constexpr bool HOOKED = !std::is_same_v<std::decay_t<Hook>, NoHook>;
     using G = Geo<C>;
     using O = Ops<C.dt>;
     using E = typename O::E;
     using E4 = typename O::E4;
     constexpr int R = G::R, R2 = G::R2;
 
-    // One LDS array per buffer: distinct objects let the compiler see that stores to one
-    // buffer never alias reads of another, so it can hoist fragment reads across stores.
-    __shared__ __attribute__((aligned(16))) E Fs[G::szFs];
-    __shared__ __attribute__((aligned(16))) E Ss[G::szSs];
-    __shared__ __attribute__((aligned(16))) E Ls[G::NBUF * G::szLs];
-    __shared__ __attribute__((aligned(16))) E Xs[G::NBUF * G::szXs];
-    __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
-    __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
-
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 15, lgrp = lane >> 4;
 
-    // Workgroups are dealt round-robin to the 8 XCDs, each with its own L2. Renumber them so
-    // that consecutive tiles (same first-core digit f, hence the same Fs slice) share an XCD;
-    // an XCD-local launch keeps only the workgroups dealt to XCD 0 (blockIdx.x % 8 == 0: with
-    // 8 * NBLK columns the linear workgroup index has the same residue modulo 8).
-    int b = blockIdx.x;
-    if constexpr (C.XL) {
-        if (b % 8 != 0) return;  // uniform per workgroup, before any barrier or access
-        b /= 8;
-    } else if constexpr (G::NBLK % 8 == 0) {
-        b = (b % 8) * (G::NBLK / 8) + b / 8;
-    }
     const int l0 = (b % G::NLC) * G::LC;
     b /= G::NLC;
     const int s0 = (b % G::NSC) * G::SC;
     const int f0 = (b / G::NSC) * G::FC;
-    const int t0 = blockIdx.y * G::TT;
+    const int t0 = tile_y * G::TT;
     // digits of each core this workgroup owns: compile-time constants when the chunks divide
     // the modes, which removes the bounds branches around the slice loads
     const int FCv = G::oF % G::FC == 0 ? G::FC : min(G::FC, G::oF - f0);
@@ -880,7 +873,8 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     // stage 1 need them, while the core slices committed after them can still be in flight.
     // (Register-resident tiles keep the slices first: their prologue is bound by the CU's
     // vector-memory rate, and measured 1-2 % faster in that order.)
-    if constexpr (!G::WIDE) issue_step(0);
+    if constexpr (HOOKED) issue_l(0);
+    else if constexpr (!G::WIDE) issue_step(0);
     // the first- and second-core slices stay resident for the whole call
     RegA<O, G::BM1, G::KF> fa;
     std::conditional_t<G::W32, RegA32<O, G::BM2, G::K2>, RegA<O, G::BM2, G::K2>> sa;
@@ -896,7 +890,12 @@ __global__ void __launch_bounds__(Geo<C>::NT)
         cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
         cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
     }
-    if constexpr (G::WIDE) issue_step(0);
+    if constexpr (HOOKED) {
+        hook();
+        issue_x(0);
+    } else if constexpr (G::WIDE) {
+        issue_step(0);
+    }
     // While the loads fly: zero what no load writes. The contiguous-iF loader writes all of
     // Xs; the scatter loader leaves the K padding, the rows iS >= nS and the rows of absent
     // tokens (TT > 1) to this fill, which writes only those.
@@ -1213,6 +1212,46 @@ __global__ void __launch_bounds__(Geo<C>::NT)
                 if (y_at(j, i, &o)) epi_put<C.dt>(y, epi_mode, o, acc[j][0].v[i], a[j][i]);
             }
     }
+}
+
+// EPI: false compiles the plain store of the plan's dtype only (epi_mode is ignored); true
+// compiles every epilogue, chosen at run time by epi_mode. Two instantiations keep the plain
+// path's code exactly as it is without epilogues (measured: a run-time branch in its store
+// loop cost up to 0.8 us at tokens 8-32).
+template <KCfg C, bool EPI>
+__global__ void __launch_bounds__(Geo<C>::NT)
+    ring3_mfma_kernel(const typename Ops<C.dt>::E *__restrict__ x,
+                      const typename Ops<C.dt>::E *__restrict__ Fk,
+                      const typename Ops<C.dt>::E *__restrict__ Sk,
+                      const typename Ops<C.dt>::E *__restrict__ Lk, void *y, int T,
+                      int epi_mode, const void *aux) {  // aux may equal y
+    // The arguments fill 14 dwords, all of which arrive preloaded in SGPRs
+    // (-amdgpu-kernarg-preload-count): one more would be fetched from the kernel-argument
+    // segment, which lives in host memory when HIP_FORCE_DEV_KERNARG=0, and the first LDS
+    // wait (lgkmcnt also counts scalar loads) would stall on that PCIe read.
+    using G = Geo<C>;
+    using E = typename Ops<C.dt>::E;
+    // One LDS array per buffer: distinct objects let the compiler see that stores to one
+    // buffer never alias reads of another, so it can hoist fragment reads across stores.
+    __shared__ __attribute__((aligned(16))) E Fs[G::szFs];
+    __shared__ __attribute__((aligned(16))) E Ss[G::szSs];
+    __shared__ __attribute__((aligned(16))) E Ls[G::NBUF * G::szLs];
+    __shared__ __attribute__((aligned(16))) E Xs[G::NBUF * G::szXs];
+    __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
+    __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
+
+    // Workgroups are dealt round-robin to the 8 XCDs, each with its own L2. Renumber them so
+    // that consecutive tiles (same first-core digit f, hence the same Fs slice) share an XCD;
+    // an XCD-local launch keeps only the workgroups dealt to XCD 0 (blockIdx.x % 8 == 0: with
+    // 8 * NBLK columns the linear workgroup index has the same residue modulo 8).
+    int b = blockIdx.x;
+    if constexpr (C.XL) {
+        if (b % 8 != 0) return;  // uniform per workgroup, before any barrier or access
+        b /= 8;
+    } else if constexpr (G::NBLK % 8 == 0) {
+        b = (b % 8) * (G::NBLK / 8) + b / 8;
+    }
+    ring3_unit<C, EPI>(x, Fk, Sk, Lk, y, T, epi_mode, aux, b, blockIdx.y, Fs, Ss, Ls, Xs, Ub, Vb);
 }
 
 template <KCfg C>

@@ -1,0 +1,31 @@
+"""The persistent multi-layer stack (kernel-task_amd/benchmarks/stack_bench.hip) on the GPU:
+L alternating 1920->2880 / 2880->1920 rank-8 layers in one launch must give bit for bit the
+output of the same tiles launched once per layer, in both forms (every XCD with device-scope
+barriers; one XCD with L2 barriers, with and without the core-slice prefetch across them),
+with no barrier reaching its spin bound. The binaries are built by __graft_entry__.build()."""
+from __future__ import annotations
+
+import importlib.util
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parents[1]
+spec = importlib.util.spec_from_file_location(
+    "stack_bench", ROOT / "kernel-task_amd" / "benchmarks" / "stack_bench.py")
+stack_bench = importlib.util.module_from_spec(spec)
+spec.loader.exec_module(stack_bench)
+
+
+@pytest.mark.parametrize("form", ["all", "xcd"])
+@pytest.mark.parametrize("tokens", [1, 3])
+def test_stack_matches_per_layer_launches(form, tokens):
+    print(f"case: stack form={form} tokens={tokens} layers=2,7", flush=True)
+    rows = stack_bench.run(form, tokens, [2, 7], timeout=120)
+    assert len(rows) == (2 if form == "all" else 4)
+    for r in rows:
+        assert r["outputs_differing"] == 0, r
+        assert r["barrier_timeouts"] == 0, r
+        assert r["outputs"] == (2880 if r["layers"] % 2 else 1920) * tokens
