@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRK_ABI_VERSION 3
+#define TRK_ABI_VERSION 4
 
 /* Element types of x, y and the cores. */
 enum trk_dtype { TRK_DTYPE_F16 = 0, TRK_DTYPE_BF16 = 1, TRK_DTYPE_F32 = 2 };
@@ -173,6 +173,20 @@ int trk_forward_variant(const trk_plan *plan, int variant, const void *packed, c
 int trk_forward_epilogue(const trk_plan *plan, int variant, const void *packed, const void *x,
                          void *y, int tokens, int epilogue, const void *aux, int aux_dtype,
                          void *stream);
+
+/* y = silu(G x) * (U x): the gate and up projections of a SwiGLU block in one launch, where
+ * `gate` and `up` are plans of one shape and dtype (created alike) and packed_gate /
+ * packed_up their packed cores. Each workgroup computes its tile of G x, keeps it in fp32
+ * registers, computes the same tile of U x and stores silu(G x) * (U x), rounded once to the
+ * dtype; nothing is allocated and no intermediate reaches memory. The variant is gate's
+ * selection for `tokens`. TRK_ERR_UNSUPPORTED when that variant has no fused kernel (fused
+ * kernels are compiled for the declared gate/up shapes: the Llama-3-8B up projection and the
+ * Qwen3.8-27B mlp_gate_up); a caller then runs the two projections with
+ * trk_forward_epilogue (TRK_EPI_F32, then TRK_EPI_SILU_MUL). Replaces the reference's
+ * three-step accumulate / accumulate / consume_silu_mul chain (csrc/v3g/bind.cu:84-136),
+ * which has no single-launch form. x, packed_gate and packed_up must be 16-byte aligned. */
+int trk_forward_swiglu(const trk_plan *gate, const void *packed_gate, const trk_plan *up,
+                       const void *packed_up, const void *x, void *y, int tokens, void *stream);
 
 /* out[i] = silu(g[i]) * u[i] for n elements: g and u fp32, out in out_dtype (rounded once).
  * g and u are only read. Replaces consume_silu_mul (csrc/v3g/bind.cu:96-110, :126-136),

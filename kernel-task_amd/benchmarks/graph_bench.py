@@ -32,6 +32,8 @@ Parts:
             consume  accumulate() x3 with the standalone consumers (the reference's
                      fp32-output chain, consume_silu_mul / consume_add)
             fused    gate.accumulate, up.forward_silu_mul, down.forward_add: 3 launches
+            pair     forward_swiglu(gate, up) (gate and up in one launch), down.forward_add:
+                     2 launches
             dense    the same block on the materialised weights (F.linear)
 """
 from __future__ import annotations
@@ -58,7 +60,9 @@ from factorized_inference import (  # noqa: E402
     tr_forward_reference,
 )
 from factorized_inference import measure as m  # noqa: E402
-from factorized_inference.tr_kernel import consume_add, consume_silu_mul  # noqa: E402
+from factorized_inference.tr_kernel import (  # noqa: E402
+    consume_add, consume_silu_mul, forward_swiglu,
+)
 
 MIB = 1 << 20
 TOL = 0.02  # the 16-bit acceptance rule |y - y_ref| <= TOL + TOL |y_ref|
@@ -288,6 +292,7 @@ MLP_FORMS = {
         consume_silu_mul(b.ring[0].accumulate(x), b.ring[1].accumulate(x), torch.bfloat16))),
     "fused": lambda b, x, h: b.ring[2].forward_add(b.ring[1].forward_silu_mul(
         x, b.ring[0].accumulate(x)), h),
+    "pair": lambda b, x, h: b.ring[2].forward_add(forward_swiglu(b.ring[0], b.ring[1], x), h),
     "dense": lambda b, x, h: h + F.linear(F.silu(F.linear(x, b.dense[0]))
                                           * F.linear(x, b.dense[1]), b.dense[2]),
 }

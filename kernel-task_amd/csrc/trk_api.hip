@@ -373,6 +373,41 @@ int trk_forward(const trk_plan *plan, const void *packed, const void *x, void *y
     return trk_forward_variant(plan, trk_plan_select(plan, tokens), packed, x, y, tokens, stream);
 }
 
+int trk_forward_swiglu(const trk_plan *gate, const void *packed_gate, const trk_plan *up,
+                       const void *packed_up, const void *x, void *y, int tokens, void *stream) {
+    if (!gate || !up) return set_error(TRK_ERR_INVALID, "trk_forward_swiglu: null plan");
+    const Plan &g = *as_plan(gate), &u = *as_plan(up);
+    if (tokens < 0) return set_error(TRK_ERR_INVALID, "trk_forward_swiglu: tokens < 0");
+    if (g.dtype != u.dtype || g.rank != u.rank || g.core_rank != u.core_rank ||
+        !std::equal(g.in_modes, g.in_modes + 3, u.in_modes) ||
+        !std::equal(g.out_modes, g.out_modes + 3, u.out_modes) || g.nchains != u.nchains ||
+        g.packed_bytes != u.packed_bytes)
+        return set_error(TRK_ERR_INVALID,
+                         "trk_forward_swiglu: the gate and up plans differ in shape, dtype, rank "
+                         "or packed layout");
+    if (tokens == 0) return TRK_OK;
+    const int variant = trk_plan_select(gate, tokens);
+    if (variant < 0 || variant >= g.nvariants)
+        return set_error(TRK_ERR_INVALID, "trk_forward_swiglu: no variant for %d tokens", tokens);
+    const Variant &v = g.variants[variant];
+    const Chain &cg = g.chains[v.chain], &cu = u.chains[v.chain];
+    if (cg.offF != cu.offF || cg.offS != cu.offS || cg.offL != cu.offL)
+        return set_error(TRK_ERR_INVALID, "trk_forward_swiglu: the plans' packed layouts differ");
+    if (!v.launch_pair)
+        return set_error(TRK_ERR_UNSUPPORTED,
+                         "trk_forward_swiglu: variant %s has no fused gate/up kernel", v.name);
+    if (!packed_gate || !packed_up || !x || !y)
+        return set_error(TRK_ERR_INVALID, "trk_forward_swiglu: null buffer");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(packed_gate) |
+         reinterpret_cast<uintptr_t>(packed_up)) & 15)
+        return set_error(TRK_ERR_INVALID,
+                         "trk_forward_swiglu: x and the packed buffers must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(y) & (g.elem - 1))
+        return set_error(TRK_ERR_INVALID, "trk_forward_swiglu: y not aligned to its element");
+    return v.launch_pair(g, v, packed_gate, packed_up, x, y, tokens,
+                         static_cast<hipStream_t>(stream));
+}
+
 int trk_consume_silu_mul(const float *g, const float *u, void *out, int out_dtype, size_t n,
                          void *stream) {
     if (n > 0 && (!g || !u || !out))

@@ -55,6 +55,10 @@ constexpr int kAuxF32 = 16;
 
 using LaunchFn = int (*)(const Plan &, const Variant &, const void *packed, const void *x,
                          void *y, int tokens, Epi epi, hipStream_t stream);
+// y = silu(G x) * (U x) for the gate and up operators of one plan layout (trk_forward_swiglu)
+using LaunchPairFn = int (*)(const Plan &, const Variant &, const void *packed_g,
+                             const void *packed_u, const void *x, void *y, int tokens,
+                             hipStream_t stream);
 
 struct Variant {
     int kind;        // trk_kernel_kind
@@ -66,6 +70,7 @@ struct Variant {
     int xcd_local;   // 1: the launch's work runs on XCD 0 only (KCfg::XL; grid x 8)
     char name[64];
     LaunchFn launch;
+    LaunchPairFn launch_pair;  // fused SwiGLU gate/up launcher, or null
 };
 
 struct Plan {

@@ -733,11 +733,17 @@ struct NoHook {
 // and before any load of x, which is then issued after it: a persistent caller's wait for the
 // layer that writes x (the core slices do not depend on it). Without a hook the loads keep
 // the standalone order.
-template <KCfg C, bool EPI, class Hook = NoHook>
+// Sections of the packed cores one pass of ring3_unit reads.
+template <class E>
+struct CoreSections {
+    const E *fk, *sk, *lk;
+};
+
+template <KCfg C, bool EPI, class Hook = NoHook, bool PAIR = false>
 __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restrict__ x,
-                                           const typename Ops<C.dt>::E *__restrict__ Fk,
-                                           const typename Ops<C.dt>::E *__restrict__ Sk,
-                                           const typename Ops<C.dt>::E *__restrict__ Lk, void *y,
+                                           const typename Ops<C.dt>::E *__restrict__ Fk0,
+                                           const typename Ops<C.dt>::E *__restrict__ Sk0,
+                                           const typename Ops<C.dt>::E *__restrict__ Lk0, void *y,
                                            int T, int epi_mode, const void *aux, int b, int tile_y,
                                            typename Ops<C.dt>::E *__restrict__ Fs,
                                            typename Ops<C.dt>::E *__restrict__ Ss,
@@ -745,13 +751,18 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
                                            typename Ops<C.dt>::E *__restrict__ Xs,
                                            typename Ops<C.dt>::E *__restrict__ Ub,
                                            typename Ops<C.dt>::E *__restrict__ Vb,
-                                           Hook &&hook = Hook{}) {
+                                           Hook &&hook = Hook{},
+                                           CoreSections<typename Ops<C.dt>::E> second = {}) {
     constexpr bool HOOKED = !std::is_same_v<std::decay_t<Hook>, NoHook>;
     using G = Geo<C>;
     using O = Ops<C.dt>;
     using E = typename O::E;
     using E4 = typename O::E4;
     constexpr int R = G::R, R2 = G::R2;
+    // the sections the current pass reads: the operator's, then (PAIR) the second one's
+    const E *__restrict__ Fk = Fk0;
+    const E *__restrict__ Sk = Sk0;
+    const E *__restrict__ Lk = Lk0;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -873,6 +884,20 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     // stage 1 need them, while the core slices committed after them can still be in flight.
     // (Register-resident tiles keep the slices first: their prologue is bound by the CU's
     // vector-memory rate, and measured 1-2 % faster in that order.)
+    // PAIR: two passes over the same tile, the first with the operator's cores, the second
+    // with `second`'s; the first pass's reduced outputs (gate) stay in registers of the waves
+    // that store, which own the same outputs in both passes, and the store writes
+    // silu(gate) * (second pass). Each pass is a whole unit: prologue, steps, reduction.
+    Acc<32> acc[G::NYW][G::NACC];
+    const int g3 = wave / G::KS3, part3 = wave % G::KS3;
+    f32x4 gate[PAIR ? G::NYW : 1];
+#pragma unroll 1
+    for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
+    if (PAIR && pass == 1) {
+        Fk = second.fk;
+        Sk = second.sk;
+        Lk = second.lk;
+    }
     if constexpr (HOOKED) issue_l(0);
     else if constexpr (!G::WIDE) issue_step(0);
     // the first- and second-core slices stay resident for the whole call
@@ -954,12 +979,10 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     auto vb_tile32 = [&](int mt, int nt) { return vb_row(mt * 32) + vb_col(nt * 32); };
     const int vb_lane32 = vb_row(4 * (lane >> 5)) + vb_col(lane & 31);
 
-    Acc<32> acc[G::NYW][G::NACC];
 #pragma unroll
     for (int j = 0; j < G::NYW; ++j)
 #pragma unroll
         for (int c = 0; c < G::NACC; ++c) acc[j][c].v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int g3 = wave / G::KS3, part3 = wave % G::KS3;
     constexpr int K3STEPS = G::K3 / 32, PERK = K3STEPS / G::KS3;
     static_assert(K3STEPS % G::KS3 == 0, "stage-3 K steps must split evenly over KS3 waves");
 
@@ -1165,6 +1188,14 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
                         red + (((p - 1) * G::G3 + g3) * G::NYW + j) * 256 + lane * 4);
         }
     }
+    if constexpr (PAIR) {
+        if (pass == 0) {
+#pragma unroll
+            for (int j = 0; j < G::NYW; ++j) gate[j] = acc[j][0].v;
+            __syncthreads();  // the next pass rewrites the LDS this one reads last
+        }
+    }
+    }  // pass
     if (part3 != 0) return;
 
     // write y[t, f, s, l] (permuted back to (p, q, r) by the compile-time strides) through
@@ -1202,7 +1233,10 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 size_t o;
-                a[j][i] = y_at(j, i, &o) ? epi_aux<C.dt>(aux, epi_mode, o) : 0.0f;
+                if constexpr (PAIR)
+                    a[j][i] = gate[j][i];
+                else
+                    a[j][i] = y_at(j, i, &o) ? epi_aux<C.dt>(aux, epi_mode, o) : 0.0f;
             }
 #pragma unroll
         for (int j = 0; j < G::NYW; ++j)
@@ -1289,11 +1323,67 @@ int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const vo
     return TRK_OK;
 }
 
+// y = silu(G x) * (U x) for two operators of one shape and plan layout (the gate and up
+// projections of a SwiGLU block) in one launch: packed_g and packed_u hold their cores at the
+// same section offsets. 12 argument dwords, all preloaded.
+template <KCfg C>
+__global__ void __launch_bounds__(Geo<C>::NT)
+    ring3_pair_kernel(const typename Ops<C.dt>::E *__restrict__ x, const char *__restrict__ packed_g,
+                      const char *__restrict__ packed_u, void *y, int offF, int offS, int offL,
+                      int T) {
+    using G = Geo<C>;
+    using E = typename Ops<C.dt>::E;
+    __shared__ __attribute__((aligned(16))) E Fs[G::szFs];
+    __shared__ __attribute__((aligned(16))) E Ss[G::szSs];
+    __shared__ __attribute__((aligned(16))) E Ls[G::NBUF * G::szLs];
+    __shared__ __attribute__((aligned(16))) E Xs[G::NBUF * G::szXs];
+    __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
+    __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
+    int b = blockIdx.x;
+    if constexpr (C.XL) {
+        if (b % 8 != 0) return;
+        b /= 8;
+    } else if constexpr (G::NBLK % 8 == 0) {
+        b = (b % 8) * (G::NBLK / 8) + b / 8;
+    }
+    const CoreSections<E> up{reinterpret_cast<const E *>(packed_u + offF),
+                             reinterpret_cast<const E *>(packed_u + offS),
+                             reinterpret_cast<const E *>(packed_u + offL)};
+    ring3_unit<C, true, NoHook, true>(x, reinterpret_cast<const E *>(packed_g + offF),
+                                      reinterpret_cast<const E *>(packed_g + offS),
+                                      reinterpret_cast<const E *>(packed_g + offL), y, T,
+                                      TRK_EPI_SILU_MUL, nullptr, b, blockIdx.y, Fs, Ss, Ls, Xs,
+                                      Ub, Vb, NoHook{}, up);
+}
+
+template <KCfg C>
+int launch_pair(const Plan &plan, const Variant &v, const void *packed_g, const void *packed_u,
+                const void *x, void *y, int tokens, hipStream_t stream) {
+    using G = Geo<C>;
+    using E = typename Ops<C.dt>::E;
+    const Chain &c = plan.chains[v.chain];
+    constexpr int kMaxTiles = 65535;
+    const int per_launch = kMaxTiles * G::TT;
+    for (int t0 = 0; t0 < tokens; t0 += per_launch) {
+        const int n = tokens - t0 < per_launch ? tokens - t0 : per_launch;
+        const dim3 grid(G::NFC * G::NSC * G::NLC * (C.XL ? 8 : 1), (n + G::TT - 1) / G::TT);
+        hipLaunchKernelGGL((ring3_pair_kernel<C>), grid, dim3(G::NT), 0, stream,
+                           static_cast<const E *>(x) + size_t(t0) * G::IN,
+                           static_cast<const char *>(packed_g), static_cast<const char *>(packed_u),
+                           static_cast<void *>(static_cast<E *>(y) + size_t(t0) * G::OUT),
+                           int(c.offF), int(c.offS), int(c.offL), n);
+        const int st = check_hip(hipGetLastError(), "trk_forward_swiglu: MFMA kernel launch");
+        if (st != TRK_OK) return st;
+    }
+    return TRK_OK;
+}
+
 struct Entry {
     KCfg cfg;
     int t_min, t_max;  // default token range (0, 0: only reachable by index)
     int lds_bytes;
     LaunchFn launch;
+    LaunchPairFn launch_pair;  // the fused SwiGLU gate/up kernel of this tile, or null
 };
 
 // One shape of the variant table (dtype, chain order, modes, rank); tile() completes it.
@@ -1307,7 +1397,11 @@ constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, in
                 TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL};
 }
 
-#define TRK_ENTRY(CFG, TMIN, TMAX) {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>},
+#define TRK_ENTRY(CFG, TMIN, TMAX) \
+    {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>, nullptr},
+// a tile of a shape that serves as the gate and up projections of SwiGLU blocks
+#define TRK_ENTRY_PAIR(CFG, TMIN, TMAX) \
+    {CFG, TMIN, TMAX, Geo<CFG>::LDS_BYTES, launch_mfma<CFG>, launch_pair<CFG>},
 
 // Appends the variants of `entries` that match the plan's shape and dtype; returns how many.
 inline int register_entries(Plan *plan, const Entry *entries, int count) {
@@ -1336,6 +1430,7 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
         v.t_min = e.t_min;
         v.t_max = e.t_max;
         v.launch = e.launch;
+        v.launch_pair = e.launch_pair;
         v.xcd_local = k.XL;
         if (k.WIDE) {
             char s1[8] = "";

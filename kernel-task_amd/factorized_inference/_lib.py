@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libtrk.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 KERNEL_GENERIC, KERNEL_MFMA = 0, 1
@@ -70,6 +70,7 @@ SIGNATURES = {
                                      _c_void_p]),
     "trk_forward_epilogue": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int,
                                       _c_int, _c_void_p, _c_int, _c_void_p]),
+    "trk_forward_swiglu": (_c_int, [_c_void_p] * 6 + [_c_int, _c_void_p]),
     "trk_consume_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_size_t,
                                       _c_void_p]),
     "trk_consume_add": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_size_t, _c_void_p]),

@@ -69,6 +69,7 @@ class ShapeDecl:
     rank: int
     dtype: str = "bf16"
     order: tuple | None = None  # chain order override (default: least padded MFMA work)
+    swiglu: bool = False  # the gate/up projections of SwiGLU blocks: compile the fused pair kernel
 
     @property
     def key(self) -> str:
@@ -124,10 +125,10 @@ QWEN = {
 BASELINE = [
     ShapeDecl("r8", (8, 12, 20), (12, 10, 24), 8, "f16", (2, 1, 0)),
     ShapeDecl("r16", (8, 12, 20), (12, 10, 24), 16, "f16", (2, 1, 0)),
-    ShapeDecl("llama_up", (16, 16, 16), (16, 28, 32), 8, "bf16"),
+    ShapeDecl("llama_up", (16, 16, 16), (16, 28, 32), 8, "bf16", swiglu=True),
     ShapeDecl("llama_down", (16, 28, 32), (16, 16, 16), 16, "bf16"),
 ]
-DECLARED = BASELINE + [ShapeDecl(f"qwen_{name}", ins, outs, rank)
+DECLARED = BASELINE + [ShapeDecl(f"qwen_{name}", ins, outs, rank, swiglu=name == "mlp_gate_up")
                        for name, (ins, outs) in QWEN.items() for rank in (8, 16)]
 
 
@@ -638,7 +639,8 @@ def emit(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fal
                      f"{shape.rank}}};")
     lines += ["", "const Entry kEntries[] = {"]
     for name, od, t, lo, hi in rows:
-        lines.append(f"    TRK_ENTRY(tile(kShape{order_tag(od)}, {t.args()}), {lo}, {hi})  // {name}")
+        macro = "TRK_ENTRY_PAIR" if shape.swiglu else "TRK_ENTRY"
+        lines.append(f"    {macro}(tile(kShape{order_tag(od)}, {t.args()}), {lo}, {hi})  // {name}")
     lines += [
         "};",
         "",

@@ -275,6 +275,30 @@ def _check_consumer_operand(name: str, t: torch.Tensor, dtype: torch.dtype | Non
     return t.contiguous()
 
 
+def forward_swiglu(gate: PreparedTRKernel, up: PreparedTRKernel, x: torch.Tensor) -> torch.Tensor:
+    """silu(gate(x)) * up(x), the gate and up projections of a SwiGLU block, in the cores'
+    dtype from one launch (trk_forward_swiglu): each workgroup computes its tile of gate(x),
+    keeps it in fp32 registers, computes the same tile of up(x) and stores the product,
+    rounded once. Where the plan's selected variant has no fused kernel (shapes other than
+    the declared gate/up ones), the same result comes from two launches:
+    up.forward_silu_mul(x, gate.accumulate(x)). Reference: the accumulate / accumulate /
+    consume_silu_mul chain of csrc/v3g/bind.cu:84-136, which takes three launches."""
+    if not isinstance(gate, PreparedTRKernel) or not isinstance(up, PreparedTRKernel):
+        raise ValueError("gate and up must be prepared operators (prepare_optimized)")
+    if (gate.spec != up.spec or gate.dtype is not up.dtype or gate.device != up.device):
+        raise ValueError("gate and up must have one shape, dtype and device")
+    x = gate._check(x)
+    y = torch.empty(x.shape[0], gate.out_features, dtype=gate.dtype, device=gate.device)
+    lib = _lib.load()
+    status = lib.trk_forward_swiglu(gate.plan.handle, gate.packed.data_ptr(), up.plan.handle,
+                                    up.packed.data_ptr(), x.data_ptr(), y.data_ptr(), x.shape[0],
+                                    current_stream_handle(gate.device_index))
+    if status == _lib.ERR_UNSUPPORTED:
+        return up.forward_silu_mul(x, gate.accumulate(x))
+    _lib.check(status)
+    return y
+
+
 def consume_silu_mul(g: torch.Tensor, u: torch.Tensor,
                      out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """silu(g) * u for fp32 g and u of one shape, rounded once to out_dtype (default bf16).

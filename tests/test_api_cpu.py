@@ -238,3 +238,29 @@ def test_plan_errors_and_variant_routing():
     assert lib.trk_forward(plan.handle, None, None, None, 1, None) == _lib.ERR_INVALID
     assert b"null buffer" in lib.trk_last_error()
     assert lib.trk_forward_variant(plan.handle, 99, 1, 1, 1, 1, None) == _lib.ERR_INVALID
+
+
+def test_forward_swiglu_argument_checks():
+    """trk_forward_swiglu checks its plans before any device work: they must agree in shape,
+    dtype and rank; a selected variant without a fused gate/up kernel is TRK_ERR_UNSUPPORTED
+    (the caller's cue to run the two-launch chain); tokens = 0 launches nothing."""
+    lib = _lib.load()
+    call = lib.trk_forward_swiglu
+    a = _lib.Plan((8, 12, 20), (12, 10, 24), 8, _lib.DTYPE_F16)
+    b = _lib.Plan((8, 12, 20), (12, 10, 24), 8, _lib.DTYPE_F16)
+    for other in (_lib.Plan((8, 12, 20), (12, 10, 24), 16, _lib.DTYPE_F16),
+                  _lib.Plan((8, 12, 20), (12, 10, 24), 8, _lib.DTYPE_BF16),
+                  _lib.Plan((8, 12, 20), (10, 12, 24), 8, _lib.DTYPE_F16)):
+        assert call(a.handle, None, other.handle, None, None, None, 1, None) == _lib.ERR_INVALID
+        assert b"differ" in lib.trk_last_error()
+    assert call(None, None, b.handle, None, None, None, 1, None) == _lib.ERR_INVALID
+    assert call(a.handle, None, b.handle, None, None, None, -1, None) == _lib.ERR_INVALID
+    assert call(a.handle, None, b.handle, None, None, None, 0, None) == _lib.OK
+    assert call(a.handle, None, b.handle, None, None, None, 1, None) == _lib.ERR_UNSUPPORTED
+    # the Llama-3-8B up projection has fused kernels in every tuned token range: past the
+    # variant check, the buffers are checked
+    g = _lib.Plan((16, 16, 16), (16, 28, 32), 8, _lib.DTYPE_BF16)
+    u = _lib.Plan((16, 16, 16), (16, 28, 32), 8, _lib.DTYPE_BF16)
+    for tokens in (1, 2, 5, 33, 200, 4096):
+        assert call(g.handle, None, u.handle, None, None, None, tokens, None) == _lib.ERR_INVALID
+        assert b"null buffer" in lib.trk_last_error()

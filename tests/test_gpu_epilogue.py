@@ -20,7 +20,7 @@ import torch.nn.functional as F
 
 from factorized_inference import TRSpec, make_cores, prepare_optimized
 from factorized_inference import _lib
-from factorized_inference.tr_kernel import consume_add, consume_silu_mul
+from factorized_inference.tr_kernel import consume_add, consume_silu_mul, forward_swiglu
 from gpu_util import TOLERANCE, check_result, oracle_y
 from oracle import ring_oracle as orc
 
@@ -30,6 +30,7 @@ DEFAULT = dict(input_modes=(8, 12, 20), output_modes=(12, 10, 24))
 LLAMA_UP = dict(input_modes=(16, 16, 16), output_modes=(16, 28, 32))
 LLAMA_DOWN = dict(input_modes=(16, 28, 32), output_modes=(16, 16, 16))
 ODD = dict(input_modes=(3, 2, 5), output_modes=(4, 3, 6))
+QWEN_GATE_UP = dict(input_modes=(20, 16, 16), output_modes=(16, 34, 32))
 
 
 def gpu_randn(shape, seed, dtype):
@@ -57,6 +58,22 @@ def check_epilogue(actual: torch.Tensor, y_ref: np.ndarray, kind: str, aux: torc
     assert actual.dtype == dtype and got.shape == expected.shape and np.isfinite(got).all()
     excess = np.abs(got - expected) - bound
     assert (excess <= 0).all(), (kind, float(excess.max()), int(np.argmax(excess)))
+
+
+def check_activation(act: torch.Tensor, g64: np.ndarray, u64: np.ndarray,
+                     dtype: torch.dtype) -> None:
+    """silu(G x) * (U x) against the oracle's gate and up outputs: both errors (each within
+    the operator's tol + tol*|.|) carried through silu(g) * u (|silu'| <= 1.1), plus one
+    rounding of the output."""
+    tol = TOLERANCE[dtype]
+    a64 = orc.epilogue("silu_mul", u64, g64)
+    got = act.double().cpu().numpy()
+    assert act.dtype == dtype and got.shape == a64.shape and np.isfinite(got).all()
+    bound = (1.1 * np.abs(u64) * (tol + tol * np.abs(g64))
+             + np.abs(orc.silu(g64)) * (tol + tol * np.abs(u64))
+             + torch.finfo(dtype).eps * np.abs(a64))
+    excess = np.abs(got - a64) - bound
+    assert (excess <= 0).all(), (float(excess.max()), int(np.argmax(excess)))
 
 
 CASES = [
@@ -226,14 +243,8 @@ def test_llama_swiglu_mlp_block():
         g64 = oracle_y(x, cg, spec_up)
         u64 = oracle_y(x, cu, spec_up)
         a64 = orc.epilogue("silu_mul", u64, g64)
-        # the activation: gate and up errors (each within tol + tol*|.|) carried through
-        # silu(g) * u (|silu'| <= 1.1), plus one rounding
-        tol = TOLERANCE[dtype]
-        got = act.double().cpu().numpy()
-        bound = (1.1 * np.abs(u64) * (tol + tol * np.abs(g64))
-                 + np.abs(orc.silu(g64)) * (tol + tol * np.abs(u64))
-                 + torch.finfo(dtype).eps * np.abs(a64))
-        assert (np.abs(got - a64) <= bound).all()
+        check_activation(act, g64, u64, dtype)
+        assert torch.equal(forward_swiglu(gate, up, x), act)
         check_epilogue(fused, oracle_y(act, cd, spec_down), "add", h, dtype)
         h64 = h.double().cpu().numpy()
         # end to end against the float64 chain without intermediate rounding: the fused
@@ -242,3 +253,49 @@ def test_llama_swiglu_mlp_block():
         err_fused = orc.errors(fused.double().cpu().numpy(), ref)["relative_l2_error"]
         err_unfused = orc.errors(unfused.double().cpu().numpy(), ref)["relative_l2_error"]
         assert err_fused <= max(1.5 * err_unfused, 5e-3), (err_fused, err_unfused)
+
+
+@pytest.mark.parametrize("shape,rank,tokens", [
+    (LLAMA_UP, 8, None),            # the first token count of every tuned range
+    (QWEN_GATE_UP, 8, (1, 3, 16)),
+    (QWEN_GATE_UP, 16, (1, 3, 16)),
+])
+def test_forward_swiglu(shape, rank, tokens):
+    """The fused gate/up launch (trk_forward_swiglu) against the two-launch chain
+    up.forward_silu_mul(x, gate.accumulate(x)), which runs the same variant, the same stage
+    code and the same fp32 gate: equal bit for bit. And against the oracle."""
+    dtype = torch.bfloat16
+    spec = TRSpec(rank=rank, **shape)
+    cg = make_cores(spec, device="cuda", dtype=dtype, seed=31, init="uniform")
+    cu = make_cores(spec, device="cuda", dtype=dtype, seed=32, init="uniform")
+    gate, up = prepare_optimized(cg, spec), prepare_optimized(cu, spec)
+    if tokens is None:
+        tokens = sorted({v["t_min"] for v in gate.variants()
+                         if v["kind"] == "mfma" and 0 < v["t_min"] <= 256})
+        assert len(tokens) >= 6
+    for T in tokens:
+        announce(test="fused gate/up", shape=shape, rank=rank, tokens=T,
+                 variant=gate.selected(T)["name"])
+        x = gpu_randn((T, spec.in_features), 70 + T, dtype)
+        fused = forward_swiglu(gate, up, x)
+        two = up.forward_silu_mul(x, gate.accumulate(x))
+        torch.cuda.synchronize()
+        assert fused.shape == (T, spec.out_features)
+        assert torch.equal(fused, two)
+        check_activation(fused, oracle_y(x, cg, spec, chunk=64), oracle_y(x, cu, spec, chunk=64),
+                         dtype)
+    assert forward_swiglu(gate, up, x[:0]).shape == (0, spec.out_features)
+
+
+def test_forward_swiglu_without_a_fused_kernel():
+    """Shapes without a fused kernel give the same result from the two-launch chain; operands
+    that do not pair are refused."""
+    spec, cores, gate = _prepare(DEFAULT, 8, torch.float16, seed=33)
+    up = prepare_optimized(make_cores(spec, device="cuda", dtype=torch.float16, seed=34), spec)
+    x = gpu_randn((5, spec.in_features), 13, torch.float16)
+    assert torch.equal(forward_swiglu(gate, up, x), up.forward_silu_mul(x, gate.accumulate(x)))
+    _, _, other = _prepare(DEFAULT, 16, torch.float16, seed=35)
+    with pytest.raises(ValueError, match="one shape"):
+        forward_swiglu(gate, other, x)
+    with pytest.raises(ValueError):
+        forward_swiglu(gate, up, x.float())
