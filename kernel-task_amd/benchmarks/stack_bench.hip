@@ -335,16 +335,25 @@ int main(int argc, char **argv) {
             std::vector<E> h1(outn), h2(outn);
             CHECK(hipMemcpy(h1.data(), y, outn * sizeof(E), hipMemcpyDeviceToHost));
             CHECK(hipMemcpy(h2.data(), yr, outn * sizeof(E), hipMemcpyDeviceToHost));
-            size_t diff = 0;
-            for (int i = 0; i < outn; ++i) diff += std::memcmp(&h1[i], &h2[i], sizeof(E)) != 0;
+            // a differing output still holding the fill pattern was never written
+            size_t diff = 0, unwritten = 0;
+            int first = -1;
+            const unsigned short fill = 0xffffu;
+            for (int i = 0; i < outn; ++i) {
+                if (std::memcmp(&h1[i], &h2[i], sizeof(E)) == 0) continue;
+                ++diff;
+                unwritten += std::memcmp(&h1[i], &fill, sizeof(E)) == 0;
+                if (first < 0) first = i;
+            }
             const float t_stack = time_us([&] { stack(L, true, pf); }, reps);
             CHECK(hipMemcpy(&herr, err, sizeof(int), hipMemcpyDeviceToHost));
             std::printf("{\"form\": \"%s\", \"prefetch\": %s, \"rank\": %d, \"tokens\": %d, \"layers\": %d, "
                         "\"workgroups\": %d, \"stack_us\": %.3f, \"barriers_only_us\": %.3f, "
                         "\"per_layer_eager_us\": %.3f, \"per_layer_graph_us\": %.3f, "
-                        "\"outputs_differing\": %zu, \"outputs\": %d, \"barrier_timeouts\": %d}\n",
+                        "\"outputs_differing\": %zu, \"differing_unwritten\": %zu, "
+                        "\"first_differing\": %d, \"outputs\": %d, \"barrier_timeouts\": %d}\n",
                         STACK_XCD ? "one_xcd" : "all_xcds", pf ? "true" : "false", R, T, L, NWG,
-                        t_stack, t_bar, t_eager, t_graph, diff, outn, herr);
+                        t_stack, t_bar, t_eager, t_graph, diff, unwritten, first, outn, herr);
         }
         CHECK(hipGraphExecDestroy(ge));
         CHECK(hipGraphDestroy(g));

@@ -782,8 +782,15 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     // Global -> LDS for one step of IC last-core input digits: the last-core slice and x are
     // read into registers (issue), then written to Ls and Xs[(iL', t, iS)][iF] (commit).
     // Every global read of a step is in flight before the first wait.
+    // Loader threads: all of them, or (pipelined tiles with the pair-and-tail stage 2) the
+    // first half. There waves 4-7, which share SIMDs 0-3 with waves 0-3, finish their stage-2
+    // tail about 500 clocks after waves 0-3 (measured): with the commit on waves 0-3 they go
+    // from stage 2 straight to the barrier (3-4 % at 1920->2880 R16, T=32 and 128). On tiles
+    // without the tail the same split measured 1-10 % slower.
+    constexpr int LT = (C.PIPE == 1 && G::TAIL) ? G::NT / 2 : G::NT;
+    const bool loader = LT == G::NT || tid < LT;
     using XV = typename VecOf<2 * G::VX>::T;
-    constexpr int XPER = G::XROW ? cdiv(G::NXV, G::NT) : cdiv(G::NXB, G::NT);
+    constexpr int XPER = G::XROW ? cdiv(G::NXV, LT) : cdiv(G::NXB, LT);
     constexpr int XREG = G::XROW ? XPER : (XPER < G::XB ? XPER : G::XB);
     XV xr[G::XROW ? XREG : 1];
     uint4 xb[G::XROW ? 1 : XREG];
@@ -794,7 +801,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
         const int n = v / G::XCPR, c = v % G::XCPR;
         const int iS = n % G::nSP, t = (n / G::nSP) % G::TT, iL = iL0 + n / (G::nSP * G::TT);
         XV r{};
-        if ((G::NXV % G::NT == 0 || v < G::NXV) && c * G::VX < G::nF && iS < G::nS &&
+        if ((G::NXV % LT == 0 || v < G::NXV) && c * G::VX < G::nF && iS < G::nS &&
             t0 + t < T)
             r = *reinterpret_cast<const XV *>(x + size_t(t0 + t) * G::IN + iS * G::SXS +
                                               iL * G::SXL + c * G::VX);
@@ -821,17 +828,18 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     };
     RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT, G::PF / 8> cF;
     RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8, G::NT, G::P2 / 8> cS;
-    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, G::NT, G::PL / 8> cL;
+    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, LT, G::PL / 8> cL;
     auto issue_l = [&](int iL0) TRK_INLINE {  // the last-core slice of the step at input digit iL0
-        cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
+        if (loader) cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
     };
     auto issue_x = [&](int iL0) TRK_INLINE {  // x for the step at input digit iL0
+        if (!loader) return;
         if constexpr (G::XROW) {
 #pragma unroll
-            for (int j = 0; j < XREG; ++j) xr[j] = x_row_load(tid + j * G::NT, iL0);
+            for (int j = 0; j < XREG; ++j) xr[j] = x_row_load(tid + j * LT, iL0);
         } else {
 #pragma unroll
-            for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * G::NT);
+            for (int j = 0; j < XREG; ++j) xb[j] = x_scatter_load(tid + j * LT);
         }
     };
     auto issue_step = [&](int iL0) TRK_INLINE {
@@ -842,29 +850,30 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     // per-register wait counts (loads complete in issue order), so loads issued after them
     // (the register-resident slices in the prologue) stay in flight.
     auto commit_l = [&](int buf) TRK_INLINE {  // into buffer `buf` of Ls
-        cL.commit(Ls + buf * G::szLs);
+        if (loader) cL.commit(Ls + buf * G::szLs);
     };
     auto commit_x = [&](int iL0, int buf) TRK_INLINE {  // into buffer `buf` of Xs
         E *xs = Xs + buf * G::szXs;
+        if (!loader) return;
         if constexpr (G::XROW) {
 #pragma unroll
             for (int j = 0; j < XREG; ++j) {
-                const int v = tid + j * G::NT;
-                if (G::NXV % G::NT == 0 || v < G::NXV)
+                const int v = tid + j * LT;
+                if (G::NXV % LT == 0 || v < G::NXV)
                     *reinterpret_cast<XV *>(xs + (v / G::XCPR) * G::PF + (v % G::XCPR) * G::VX) =
                         xr[j];
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < XREG; ++j) x_scatter_store(tid + j * G::NT, xb[j], iL0, xs);
+            for (int j = 0; j < XREG; ++j) x_scatter_store(tid + j * LT, xb[j], iL0, xs);
             for (int j0 = XREG; j0 < XPER; j0 += XREG) {  // further batches, one latency each
 #pragma unroll
                 for (int j = 0; j < XREG; ++j)
-                    xb[j] = j0 + j < XPER ? x_scatter_load(tid + (j0 + j) * G::NT)
+                    xb[j] = j0 + j < XPER ? x_scatter_load(tid + (j0 + j) * LT)
                                           : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
                 for (int j = 0; j < XREG; ++j)
-                    if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * G::NT, xb[j], iL0, xs);
+                    if (j0 + j < XPER) x_scatter_store(tid + (j0 + j) * LT, xb[j], iL0, xs);
             }
         }
     };
@@ -883,7 +892,8 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     // LDS-staged tiles issue the first step's last-core slice and x first: the commit and
     // stage 1 need them, while the core slices committed after them can still be in flight.
     // (Register-resident tiles keep the slices first: their prologue is bound by the CU's
-    // vector-memory rate, and measured 1-2 % faster in that order.)
+    // vector-memory rate, and measured 1-2 % faster in that order. The exception are the
+    // tiles with half-workgroup loaders, 1 % faster with the step's slices first.)
     // PAIR: two passes over the same tile, the first with the operator's cores, the second
     // with `second`'s; the first pass's reduced outputs (gate) stay in registers of the waves
     // that store, which own the same outputs in both passes, and the store writes
@@ -898,8 +908,9 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
         Sk = second.sk;
         Lk = second.lk;
     }
+    constexpr bool STEP_FIRST = !G::WIDE || LT < G::NT;
     if constexpr (HOOKED) issue_l(0);
-    else if constexpr (!G::WIDE) issue_step(0);
+    else if constexpr (STEP_FIRST) issue_step(0);
     // the first- and second-core slices stay resident for the whole call
     RegA<O, G::BM1, G::KF> fa;
     std::conditional_t<G::W32, RegA32<O, G::BM2, G::K2>, RegA<O, G::BM2, G::K2>> sa;
@@ -918,7 +929,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     if constexpr (HOOKED) {
         hook();
         issue_x(0);
-    } else if constexpr (G::WIDE) {
+    } else if constexpr (!STEP_FIRST) {
         issue_step(0);
     }
     // While the loads fly: zero what no load writes. The contiguous-iF loader writes all of

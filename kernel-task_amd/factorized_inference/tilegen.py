@@ -465,8 +465,9 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
                 if ic > c.nL or c.nL % ic:
                     continue
                 # (2 tokens: twice the inputs per step in the LDS of 4 tokens' tiles; measured
-                # 5 % faster for Llama down at 32 tokens)
-                for tt, ks3, nacc in ((4, 2, 1), (4, 1, 2), (2, 1, 2), (2, 2, 1)):
+                # 5 % faster for Llama down at 32 tokens; stage 3 split four ways puts its two
+                # output tiles on all 8 waves)
+                for tt, ks3, nacc in ((4, 2, 1), (4, 1, 2), (2, 1, 2), (2, 2, 1), (2, 4, 1)):
                     t = Tile(tt, 1, base.SC, LC, ic, ks3, nacc, wide, 32, nw)
                     if not geometry(shape, order, t)["reject"] and t not in out.values():
                         out[f"{fam}_t{tt}k{ks3}n{nacc}_ic{ic}"] = t

@@ -26,6 +26,8 @@ def test_stack_matches_per_layer_launches(form, tokens):
     rows = stack_bench.run(form, tokens, [2, 7], timeout=120)
     assert len(rows) == (2 if form == "all" else 4)
     for r in rows:
+        print(r, flush=True)
+    for r in rows:
         assert r["outputs_differing"] == 0, r
         assert r["barrier_timeouts"] == 0, r
         assert r["outputs"] == (2880 if r["layers"] % 2 else 1920) * tokens
