@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <random>
+#include <string>
 #include <vector>
 
 #include "trk.h"
@@ -157,12 +158,18 @@ __device__ __forceinline__ void run_layer(const Layer &lay, const E *in, E *out,
 template <bool WORK, bool PREFETCH>
 __global__ void __launch_bounds__(NT)
     stack_kernel(const E *x, E *act0, E *act1, E *y, const Layer *layers, int L, int T,
-                 unsigned *counter, unsigned base, int *err, int spin) {
+                 unsigned *counter, unsigned base, int *err, int spin, unsigned *xcc) {
     __shared__ __attribute__((aligned(16))) E pool[POOL];
     int wg = blockIdx.x;
     if constexpr (STACK_XCD) {
         if (wg % 8 != 0) return;  // dealt to XCDs 1-7
         wg /= 8;
+        // the XCD this workgroup runs on (hardware register XCC_ID, bits 3:0): the host
+        // checks that the dealing put every working workgroup on one XCD, which the L2
+        // barrier assumes
+        unsigned id;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(id));
+        if (threadIdx.x == 0) xcc[wg] = id & 0xfu;
     }
     for (int l = 0; l < L; ++l) {
         const E *in = l == 0 ? x : ((l - 1) & 1 ? act1 : act0);
@@ -252,9 +259,10 @@ int main(int argc, char **argv) {
     CHECK(hipMalloc(&x, hx.size() * sizeof(E)));
     CHECK(hipMemcpy(x, hx.data(), hx.size() * sizeof(E), hipMemcpyHostToDevice));
     for (E **p : {&a0, &a1, &y, &yr, &b0, &b1}) CHECK(hipMalloc(p, size_t(T) * MAXF * sizeof(E)));
-    unsigned *counter;
+    unsigned *counter, *xcc;
     int *err;
     CHECK(hipMalloc(&counter, sizeof(unsigned)));
+    CHECK(hipMalloc(&xcc, sizeof(unsigned) * NWG));
     CHECK(hipMalloc(&err, sizeof(int)));
     CHECK(hipMemset(counter, 0, sizeof(unsigned)));
     CHECK(hipMemset(err, 0, sizeof(int)));
@@ -278,7 +286,7 @@ int main(int argc, char **argv) {
     };
     auto stack = [&](int L, bool work, bool prefetch) {
         int Ti = T, Li = L, spini = spin;
-        void *args[] = {&x, &a0, &a1, &y, &dlayers, &Li, &Ti, &counter, &base, &err, &spini};
+        void *args[] = {&x, &a0, &a1, &y, &dlayers, &Li, &Ti, &counter, &base, &err, &spini, &xcc};
         const void *fn = work ? (prefetch ? (const void *)stack_kernel<true, true>
                                           : (const void *)stack_kernel<true, false>)
                               : (const void *)stack_kernel<false, false>;
@@ -322,6 +330,7 @@ int main(int argc, char **argv) {
             const bool pf = prefetch_modes[m];
             // correctness: bitwise against the per-layer launches of the same tiles
             CHECK(hipMemset(y, 0xff, size_t(T) * MAXF * sizeof(E)));
+            CHECK(hipMemset(xcc, 0xff, sizeof(unsigned) * NWG));
             stack(L, true, pf);
             per_layer(L, nullptr);
             CHECK(hipDeviceSynchronize());
@@ -331,6 +340,12 @@ int main(int argc, char **argv) {
                 std::printf("{\"error\": \"a barrier reached its spin bound\", \"L\": %d}\n", L);
                 return 3;
             }
+            std::vector<unsigned> hids(NWG);
+            CHECK(hipMemcpy(hids.data(), xcc, sizeof(unsigned) * NWG, hipMemcpyDeviceToHost));
+            std::sort(hids.begin(), hids.end());
+            hids.erase(std::unique(hids.begin(), hids.end()), hids.end());
+            std::string ids;
+            for (unsigned v : hids) ids += (ids.empty() ? "" : ", ") + std::to_string(int(v));
             const int outn = (L % 2 == 1 ? 2880 : 1920) * T;
             std::vector<E> h1(outn), h2(outn);
             CHECK(hipMemcpy(h1.data(), y, outn * sizeof(E), hipMemcpyDeviceToHost));
@@ -351,15 +366,18 @@ int main(int argc, char **argv) {
                         "\"workgroups\": %d, \"stack_us\": %.3f, \"barriers_only_us\": %.3f, "
                         "\"per_layer_eager_us\": %.3f, \"per_layer_graph_us\": %.3f, "
                         "\"outputs_differing\": %zu, \"differing_unwritten\": %zu, "
-                        "\"first_differing\": %d, \"outputs\": %d, \"barrier_timeouts\": %d}\n",
+                        "\"first_differing\": %d, \"outputs\": %d, \"barrier_timeouts\": %d, "
+                        "\"xcd_ids\": [%s]}\n",
                         STACK_XCD ? "one_xcd" : "all_xcds", pf ? "true" : "false", R, T, L, NWG,
-                        t_stack, t_bar, t_eager, t_graph, diff, unwritten, first, outn, herr);
+                        t_stack, t_bar, t_eager, t_graph, diff, unwritten, first, outn, herr,
+                        STACK_XCD ? ids.c_str() : "");
         }
         CHECK(hipGraphExecDestroy(ge));
         CHECK(hipGraphDestroy(g));
         CHECK(hipStreamDestroy(cs));
     }
     for (void *p : owned) CHECK(hipFree(p));
+    CHECK(hipFree(xcc));
     trk_plan_destroy(pu);
     trk_plan_destroy(pd);
     return 0;

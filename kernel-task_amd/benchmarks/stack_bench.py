@@ -86,7 +86,8 @@ def main() -> int:
                   f"{r['barriers_only_us'] / r['layers']:.3f}, per-layer eager "
                   f"{r['per_layer_eager_us'] / r['layers']:.3f}, graph "
                   f"{r['per_layer_graph_us'] / r['layers']:.3f}; outputs differing "
-                  f"{r['outputs_differing']} of {r['outputs']}", flush=True)
+                  f"{r['outputs_differing']} of {r['outputs']}"
+                  + (f"; XCDs {r['xcd_ids']}" if r["xcd_ids"] else ""), flush=True)
     if args.out:
         args.out.parent.mkdir(parents=True, exist_ok=True)
         args.out.write_text(json.dumps({"rows": rows}, indent=1) + "\n")
