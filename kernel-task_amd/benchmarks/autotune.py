@@ -95,7 +95,8 @@ EAGER_FROM_US = 12.0  # tiles this slow (graph-timed) are re-timed with eager ca
 
 
 def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
-    dtype = torch.bfloat16 if shape.dtype == "bf16" else torch.float16
+    dtype = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[shape.dtype]
+    tol = 1e-4 if dtype is torch.float32 else 0.02  # the acceptance rule of the dtype
     spec = TRSpec(shape.ins, shape.outs, shape.rank)
     cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init="uniform")
     run = prepare_optimized(cores, spec)
@@ -118,7 +119,7 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
             y = run.run_variant(x, i).float()
             torch.cuda.synchronize()
             err = (y - ref).abs().max().item()
-            if not (err <= 0.02 * scale + 0.02):  # a tile that disagrees never wins
+            if not (err <= tol * scale + tol):  # a tile that disagrees never wins
                 print(f"  {shape.key} T={T} {v['name']}: disagrees ({err:.3e}), skipped",
                       flush=True)
                 continue

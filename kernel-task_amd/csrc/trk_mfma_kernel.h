@@ -98,6 +98,33 @@ struct Ops<TRK_DTYPE_BF16> {
     }
 };
 
+// fp32: the same fragments (8 or 4 K-consecutive elements per lane) as sequences of fp32
+// MFMAs of K 4 (16x16x4) or 2 (32x32x2), each taking one element per lane: step q runs the K
+// positions {q, 8 + q, 16 + q, 24 + q} (16x16x32 fragment) or {q, 8 + q} (32x32x16), so the
+// sum over q covers the fragment's K range once, in full fp32 (no reduced-precision inputs).
+template <>
+struct Ops<TRK_DTYPE_F32> {
+    using E = float;
+    using V8 = float __attribute__((ext_vector_type(8)));
+    using V4 = float __attribute__((ext_vector_type(4)));
+    using E4 = V4;
+    __device__ static Acc<32> k32(V8 a, V8 b, Acc<32> c) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) c.v = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q], b[q], c.v, 0, 0, 0);
+        return c;
+    }
+    __device__ static Acc<16> k16(V4 a, V4 b, Acc<16> c) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c.v = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q], b[q], c.v, 0, 0, 0);
+        return c;
+    }
+    __device__ static f32x16 w16(V8 a, V8 b, f32x16 c) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q], b[q], c, 0, 0, 0);
+        return c;
+    }
+};
+
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int rup(int a, int b) { return cdiv(a, b) * b; }
 constexpr int pick(int m, int a, int b, int c) { return m == 0 ? a : (m == 1 ? b : c); }
@@ -247,6 +274,8 @@ struct Geo {
     static constexpr int SYS = pick(C.S, C.o1 * C.o2, C.o2, 1);
     static constexpr int SYL = pick(C.L, C.o1 * C.o2, C.o2, 1);
     static constexpr int KF = rup(nF, 16), K2 = rup(nS * R, 16);
+    // element bytes, and elements per 16-byte vector (the unit of the global <-> LDS copies)
+    static constexpr int EB = C.dt == TRK_DTYPE_F32 ? 4 : 2, VPE = 16 / EB;
     static constexpr int TT = C.TT, FC = C.FC, SC = C.SC, LC = C.LC, IC = C.IC, KS3 = C.KS3;
     static constexpr int NACC = C.NACC;
     static constexpr bool WIDE = C.WIDE != 0;
@@ -297,7 +326,7 @@ struct Geo {
     // in LDS with them; otherwise 16 bytes past each K extent (conflict free for 32x32 reads)
     static constexpr bool CFP =
         lds_elems(WIDE, M1, M2P, IC * LCP, N1P, N2R, M3P, SC, NBUF, NBUF2, pitch16(KF),
-                  W32 ? pitch32(K2) : pitch16(K2), pitch16(K3), pitch16(R2)) * 2 <= 160 * 1024;
+                  W32 ? pitch32(K2) : pitch16(K2), pitch16(K3), pitch16(R2)) * EB <= 160 * 1024;
     static constexpr int PF = CFP ? pitch16(KF) : KF + 8;
     static constexpr int P2 = W32 ? pitch32(K2) : CFP ? pitch16(K2) : K2 + 8;
     static constexpr int PL = CFP ? pitch16(R2) : R2 + 8;
@@ -314,21 +343,26 @@ struct Geo {
     static constexpr int VBL = vb_layout(W32, Q, R, LG, K3, CFP ? pitch16(K3) : K3 + 8, SC, M3T);
     static constexpr int P3 = VBL / 256, PLANE_PAD = SC * P3 + VBL % 256;
     static constexpr int PLANE =
-        (oVb + NBUF2 * vb_elems(M3P, SC, P3, PLANE_PAD)) * 2 <= 160 * 1024 ? PLANE_PAD : SC * P3;
+        (oVb + NBUF2 * vb_elems(M3P, SC, P3, PLANE_PAD)) * EB <= 160 * 1024 ? PLANE_PAD : SC * P3;
     static constexpr int szVb = vb_elems(M3P, SC, P3, PLANE);
     static constexpr int LDS_ELEMS = oVb + NBUF2 * szVb;
-    static constexpr int LDS_BYTES = LDS_ELEMS * 2;
+    static constexpr int LDS_BYTES = LDS_ELEMS * EB;
     static constexpr int RED_FLOATS = (KS3 - 1) * G3 * NYW * 256;
-    // x loader. Contiguous iF: VX-element vectors straight into Xs rows. Otherwise: 8-element
-    // vectors of the natural x row, scattered element by element, in batches of XB per thread.
+    // x loader. Contiguous iF: VX-element vectors straight into Xs rows. Otherwise: 16-byte
+    // vectors (VPE elements) of the natural x row, scattered element by element, in batches of
+    // XB per thread.
     static constexpr bool XROW = SXF == 1;
     static constexpr int vx_fits(int v) {
         return nF % v == 0 && SXS % v == 0 && SXL % v == 0 && IN % v == 0;
     }
-    static constexpr int VX = !XROW ? 1 : vx_fits(8) ? 8 : vx_fits(4) ? 4 : vx_fits(2) ? 2 : 1;
+    static constexpr int VX = !XROW                     ? 1
+                              : VPE >= 8 && vx_fits(8) ? 8
+                              : vx_fits(4)             ? 4
+                              : vx_fits(2)             ? 2
+                                                       : 1;
     static constexpr int XCPR = KF / VX;                      // vectors per Xs row (contiguous iF)
     static constexpr int NXV = N1 * XCPR;                     // vectors per step (contiguous iF)
-    static constexpr int NXB = TT * IN / 8;                   // vectors per step (scatter)
+    static constexpr int NXB = TT * IN / VPE;                 // vectors per step (scatter)
     static constexpr int XB = 8;
 
     static_assert(R % 8 == 0 && (R & (R - 1)) == 0, "MFMA variants need a power-of-two rank >= 8");
@@ -342,13 +376,13 @@ struct Geo {
     static_assert(NACC >= 1 && (K3 / 32 / KS3) % NACC == 0, "NACC must divide a wave's K steps");
     static_assert(FC <= oF && SC <= oS && LC <= oL && IC <= nL && TT >= 1, "tile too large");
     static_assert(LDS_BYTES <= 160 * 1024, "workgroup tile exceeds the 160 KB of LDS");
-    static_assert(RED_FLOATS * 4 <= szUb * 2, "stage-3 reduction does not fit in Ub");
+    static_assert(RED_FLOATS * 4 <= szUb * EB, "stage-3 reduction does not fit in Ub");
     static_assert(nL % IC == 0, "IC must divide the last core's input mode");
     static_assert(R % SG == 0 && R % LG == 0 && SG % 4 == 0 && LG % 4 == 0,
                   "K-order groups must hold whole 4-element stores");
     static_assert(C.PIPE >= 0 && C.PIPE <= 2 && (C.PIPE == 0 || NSTEP > 1),
                   "a pipelined tile needs two steps");
-    static_assert(XROW || IN % 8 == 0, "scatter loader reads x rows in 8-element vectors");
+    static_assert(XROW || IN % VPE == 0, "scatter loader reads x rows in 16-byte vectors");
     static_assert(C.S1 == 0 || (WIDE && M1T % C.S1 == 0 && NW % (M1T / C.S1) == 0),
                   "S1 must split the stage-1 rows into a divisor of the waves");
 };
@@ -789,7 +823,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     // without the tail the same split measured 1-10 % slower.
     constexpr int LT = (C.PIPE == 1 && G::TAIL) ? G::NT / 2 : G::NT;
     const bool loader = LT == G::NT || tid < LT;
-    using XV = typename VecOf<2 * G::VX>::T;
+    using XV = typename VecOf<G::EB * G::VX>::T;
     constexpr int XPER = G::XROW ? cdiv(G::NXV, LT) : cdiv(G::NXB, LT);
     constexpr int XREG = G::XROW ? XPER : (XPER < G::XB ? XPER : G::XB);
     XV xr[G::XROW ? XREG : 1];
@@ -809,28 +843,29 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     };
     auto x_scatter_load = [&](int v) TRK_INLINE {       // scatter loader: 8 contiguous x elements
         uint4 r = make_uint4(0u, 0u, 0u, 0u);
-        if (v < G::NXB && t0 + v / (G::IN / 8) < T)
+        if (v < G::NXB && t0 + v / (G::IN / G::VPE) < T)
             r = reinterpret_cast<const uint4 *>(x + size_t(t0) * G::IN)[v];
         return r;
     };
     auto x_scatter_store = [&](int v, uint4 r, int iL0, E *xs) TRK_INLINE {
-        const int t = v / (G::IN / 8);
+        const int t = v / (G::IN / G::VPE);
         if (v >= G::NXB || t0 + t >= T) return;
         const E *e = reinterpret_cast<const E *>(&r);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int flat = (v % (G::IN / 8)) * 8 + q;
+        for (int q = 0; q < G::VPE; ++q) {
+            const int flat = (v % (G::IN / G::VPE)) * G::VPE + q;
             const int m0 = flat / (C.i1 * C.i2), m1 = (flat / C.i2) % C.i1, m2 = flat % C.i2;
             const int iF = pick(C.F, m0, m1, m2), iS = pick(C.S, m0, m1, m2);
             const int ilp = pick(C.L, m0, m1, m2) - iL0;
             if (ilp >= 0 && ilp < G::IC) xs[((ilp * G::TT + t) * G::nSP + iS) * G::PF + iF] = e[q];
         }
     };
-    RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / 8, G::WIDE ? 1 : G::KF / 8, G::NT, G::PF / 8> cF;
-    RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / 8, G::WIDE ? 1 : G::K2 / 8, G::NT, G::P2 / 8> cS;
-    RegCopy<G::IC, G::LCP * R2 / 8, R2 / 8, LT, G::PL / 8> cL;
+    constexpr int VPE = G::VPE;
+    RegCopy<1, G::WIDE ? 1 : G::M1 * G::KF / VPE, G::WIDE ? 1 : G::KF / VPE, G::NT, G::PF / VPE> cF;
+    RegCopy<1, G::WIDE ? 1 : G::M2P * G::K2 / VPE, G::WIDE ? 1 : G::K2 / VPE, G::NT, G::P2 / VPE> cS;
+    RegCopy<G::IC, G::LCP * R2 / VPE, R2 / VPE, LT, G::PL / VPE> cL;
     auto issue_l = [&](int iL0) TRK_INLINE {  // the last-core slice of the step at input digit iL0
-        if (loader) cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / 8, LCv * R2 / 8);
+        if (loader) cL.issue(Lk + (size_t(iL0) * G::oL + l0) * R2, size_t(G::oL) * R2 / VPE, LCv * R2 / VPE);
     };
     auto issue_x = [&](int iL0) TRK_INLINE {  // x for the step at input digit iL0
         if (!loader) return;
@@ -923,8 +958,8 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
         else
             sa.load(Sk + size_t(s0) * R * G::K2, wm2 * G::BM2 * 16, SCv * R, lrow, lgrp);
     } else {
-        cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / 8);
-        cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / 8);
+        cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / VPE);
+        cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / VPE);
     }
     if constexpr (HOOKED) {
         hook();
@@ -936,15 +971,15 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     // Xs; the scatter loader leaves the K padding, the rows iS >= nS and the rows of absent
     // tokens (TT > 1) to this fill, which writes only those.
     if constexpr (!G::XROW && (G::KF > G::nF || G::nSP > G::nS || G::TT > 1)) {
-        constexpr int CH = G::KF / 8;  // 16-byte chunks per row
+        constexpr int CH = G::KF / VPE;  // 16-byte chunks per row
         for (int i = tid; i < G::NBUF * G::N1 * CH; i += G::NT) {  // every buffer of Xs
             const int b = i / (G::N1 * CH), n = (i / CH) % G::N1, c = i % CH;
             E *xs = Xs + b * G::szXs;
             const bool empty_row = n % G::nSP >= G::nS || t0 + (n / G::nSP) % G::TT >= T;
-            if (empty_row || 8 * c >= G::nF) {
-                *reinterpret_cast<uint4 *>(xs + n * G::PF + 8 * c) = make_uint4(0u, 0u, 0u, 0u);
-            } else if (G::nF % 8 != 0 && 8 * c + 8 > G::nF) {
-                for (int e = G::nF; e < 8 * c + 8; ++e) xs[n * G::PF + e] = E(0.0f);
+            if (empty_row || VPE * c >= G::nF) {
+                *reinterpret_cast<uint4 *>(xs + n * G::PF + VPE * c) = make_uint4(0u, 0u, 0u, 0u);
+            } else if (G::nF % VPE != 0 && VPE * c + VPE > G::nF) {
+                for (int e = G::nF; e < VPE * c + VPE; ++e) xs[n * G::PF + e] = E(0.0f);
             }
         }
     }

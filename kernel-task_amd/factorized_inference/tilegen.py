@@ -42,7 +42,8 @@ CSRC = PACKAGE.parent / "csrc"
 GEN_DIR = CSRC / "gen"
 TUNED = GEN_DIR / "tuned.json"
 
-DTYPES = {"f16": "TRK_DTYPE_F16", "bf16": "TRK_DTYPE_BF16"}
+DTYPES = {"f16": "TRK_DTYPE_F16", "bf16": "TRK_DTYPE_BF16", "f32": "TRK_DTYPE_F32"}
+ELEM_BYTES = {"f16": 2, "bf16": 2, "f32": 4}
 LDS_LIMIT = 160 * 1024
 # registers a wave may give to the register-resident core slices (4 waves: one wave per
 # SIMD; 8 waves: two per SIMD, half the register file each)
@@ -121,12 +122,14 @@ QWEN = {
     "gdn_qkvz": ((20, 16, 16), (16, 32, 32)),
 }
 # The BASELINE configs: 1920 -> 2880 at ranks 8 and 16 in fp16 (chain order (G3, G2, G1), whose
-# stage-1 x reads are contiguous in iF), and the Llama-3-8B up/down projections in bf16.
+# stage-1 x reads are contiguous in iF), the Llama-3-8B up/down projections in bf16, and
+# 1920 -> 2880 at rank 8 in fp32 (config 1, the reference's CPU case; fp32 MFMAs here).
 BASELINE = [
     ShapeDecl("r8", (8, 12, 20), (12, 10, 24), 8, "f16", (2, 1, 0)),
     ShapeDecl("r16", (8, 12, 20), (12, 10, 24), 16, "f16", (2, 1, 0)),
     ShapeDecl("llama_up", (16, 16, 16), (16, 28, 32), 8, "bf16", swiglu=True),
     ShapeDecl("llama_down", (16, 28, 32), (16, 16, 16), 16, "bf16"),
+    ShapeDecl("r8_fp32", (8, 12, 20), (12, 10, 24), 8, "f32", (2, 1, 0)),
 ]
 DECLARED = BASELINE + [ShapeDecl(f"qwen_{name}", ins, outs, rank, swiglu=name == "mlp_gate_up")
                        for name, (ins, outs) in QWEN.items() for rank in (8, 16)]
@@ -251,6 +254,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     kernel would reject it ("" when it compiles). Mirrors the static_asserts of Geo."""
     c, R = chain_of(shape, order), shape.rank
     R2 = R * R
+    eb = ELEM_BYTES[shape.dtype]
     g = {}
     KF, K2, nSP = rup(c.nF, 16), rup(c.nS * R, 16), rup(c.nS, 16)
     M1 = t.FC * R2
@@ -283,8 +287,8 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         return ((16 if wide else M1 * pf + M2P * p2) + nbuf * (t.IC * LCP * pl + N1 * pf)
                 + nbuf2 * (N2R * p2 + vb))
     # pitches for the fragment shape each buffer is read with, where the tile fits with them
-    cfp = 2 * lds_elems(pitch16(KF), pitch32(K2) if W32 else pitch16(K2), pitch16(K3),
-                        pitch16(R2)) <= LDS_LIMIT
+    cfp = eb * lds_elems(pitch16(KF), pitch32(K2) if W32 else pitch16(K2), pitch16(K3),
+                         pitch16(R2)) <= LDS_LIMIT
     PF, PL = (pitch16(KF), pitch16(R2)) if cfp else (KF + 8, R2 + 8)
     P2 = pitch32(K2) if W32 else pitch16(K2) if cfp else K2 + 8
     M2T32, N2T32 = cdiv(M2, 32), cdiv(N2, 32)
@@ -307,21 +311,23 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     P3, pad = vb_layout(W32, t.TT * t.FC, R, lg, K3, pitch16(K3) if cfp else K3 + 8, t.SC, M3T)
     vb = lambda plane: nbuf2 * ((M3P - 1) // t.SC * plane + ((M3P - 1) % t.SC + 1) * P3)  # noqa: E731
     sz["Vb"] = vb(t.SC * P3 + pad)
-    if 2 * sum(sz.values()) > LDS_LIMIT:
+    if eb * sum(sz.values()) > LDS_LIMIT:
         sz["Vb"] = vb(t.SC * P3)
-    lds = 2 * sum(sz.values())
+    lds = eb * sum(sz.values())
     red_floats = (t.KS3 - 1) * G3 * NYW * 256
     k3steps = K3 // 32 if K3 % 32 == 0 else 0
     perk = k3steps // t.KS3 if t.KS3 else 0
     qb = min(perk, 16)
     g.update(LDS_BYTES=lds, NBLK=cdiv(c.oF, t.FC) * cdiv(c.oS, t.SC) * cdiv(c.oL, t.LC),
              NSTEP=cdiv(c.nL, t.IC), BM1=BM1, BM2=BM2, NYW=NYW, K2=K2, KF=KF)
-    # register-resident slices (WIDE): A fragments held by each wave
+    # register-resident slices (WIDE): A fragments held by each wave (an 8-element fragment
+    # is 4 VGPRs in 16 bits, 8 in fp32)
     if wide:
+        v8 = 2 * eb
         # a trailing 16 of K after 32-wide steps is held as a full 8-element fragment
-        tail = lambda k: (4 if k >= 32 else 2) if k % 32 else 0  # noqa: E731
-        fa = BM1 * (KF // 32 * 4 + tail(KF))
-        sa = BM2 * (K2 // 16) * 4 if W32 else BM2 * (K2 // 32 * 4 + tail(K2))
+        tail = lambda k: (v8 if k >= 32 else v8 // 2) if k % 32 else 0  # noqa: E731
+        fa = BM1 * (KF // 32 * v8 + tail(KF))
+        sa = BM2 * (K2 // 16) * v8 if W32 else BM2 * (K2 // 32 * v8 + tail(K2))
         g["slice_vgprs"] = fa + sa
     checks = [
         (R % 8 == 0 and R & (R - 1) == 0, "rank must be a power of two >= 8"),
@@ -339,9 +345,9 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (t.PIPE in (0, 1, 2) and (t.PIPE == 0 or c.nL // t.IC > 1), "a pipelined tile needs two steps"),
         (t.S1 == 0 or (wide and WM1 > 0 and NW % WM1 == 0), "S1 must split the stage-1 rows"),
         (t.XL in (0, 1), "XL is 0 or 1"),
-        (c.xrow or c.IN % 8 == 0, "scatter loader reads x rows in 8-element vectors"),
+        (c.xrow or c.IN % (16 // eb) == 0, "scatter loader reads x rows in 16-byte vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
-        (red_floats * 4 <= N2R * P2 * 2, "stage-3 reduction does not fit in Ub"),
+        (red_floats * 4 <= N2R * P2 * eb, "stage-3 reduction does not fit in Ub"),
         (not wide or g["slice_vgprs"] <= WIDE_VGPR_RELAXED[NW],
          "register-resident slices too large"),
     ]

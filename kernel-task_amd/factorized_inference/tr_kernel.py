@@ -4,7 +4,7 @@ Mirrors src/factorized_inference/tr_kernel.py of the reference (PreparedTRKernel
 prepare time, a tiling/variant choice per token count) with its own mechanics:
 
   prepare  trk_plan_create picks the contraction order(s) and kernel variants for the shape;
-           a 16-bit shape without compiled MFMA tables gets a variant module built for it
+           a shape without compiled MFMA tables gets a variant module built for it
            (jit.py: the generator's table compiled once, cached), at the next power-of-two
            kernel rank when the cores' rank has none (zero-padded ring links, exact);
            trk_pack packs the cores into one device buffer (no dense W, padding only)
@@ -36,6 +36,7 @@ from .reference import TRSpec, _validate_cores
 
 _DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16,
            torch.float32: _lib.DTYPE_F32}
+_TILEGEN_DTYPES = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 if _raw_stream is None:
@@ -67,14 +68,13 @@ def _torch_call():
 
 
 def make_plan(spec: TRSpec, dtype: torch.dtype) -> _lib.Plan:
-    """The plan of one operator: the library's own variant tables; for fp16/bf16 shapes
-    without MFMA variants, a plan at the MFMA kernel rank (trk_plan_create_padded when the
-    cores' rank is not a power of two >= 8) with a variant module built for the shape
-    (jit.build_module). Shapes the generator has no tile for, fp32, and TRK_JIT=0 keep the
-    generic HIP kernel."""
+    """The plan of one operator: the library's own variant tables; for shapes without MFMA
+    variants, a plan at the MFMA kernel rank (trk_plan_create_padded when the cores' rank is
+    not a power of two >= 8) with a variant module built for the shape (jit.build_module).
+    Shapes the generator has no tile for and TRK_JIT=0 keep the generic HIP kernel."""
     code = _DTYPES[dtype]
     plan = _lib.Plan(spec.input_modes, spec.output_modes, spec.rank, code)
-    if dtype is torch.float32 or plan.has_mfma or not jit.enabled():
+    if plan.has_mfma or not jit.enabled():
         return plan
     krank = jit.kernel_rank(spec.rank)
     if krank is None:
@@ -83,7 +83,7 @@ def make_plan(spec: TRSpec, dtype: torch.dtype) -> _lib.Plan:
         spec.input_modes, spec.output_modes, spec.rank, code, kernel_rank=krank)
     if not padded.has_mfma:
         shape = tilegen.ShapeDecl("prepared", tuple(spec.input_modes), tuple(spec.output_modes),
-                                  krank, "f16" if dtype is torch.float16 else "bf16")
+                                  krank, _TILEGEN_DTYPES[dtype])
         try:
             path = jit.build_module(shape)
         except (OSError, RuntimeError) as exc:

@@ -48,11 +48,14 @@ def test_undeclared_shapes_get_mfma_variants(ins, outs, rank, dtype):
     for tokens in (1, 8, 64, 1000):
         assert plan.describe(-1, tokens)["kind"] == "mfma", tokens
     # the work reported is the rank-`rank` operator's, whatever rank the kernels run at
-    unpadded = _lib.Plan(ins, outs, rank, 0 if dt is torch.float16 else 1)
+    code = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16,
+            torch.float32: _lib.DTYPE_F32}[dt]
+    unpadded = _lib.Plan(ins, outs, rank, code)
     for tokens in (1, 7):
         assert plan.describe(-1, tokens)["bytes"] == unpadded.describe(0, tokens)["bytes"]
     params = sum(rank * rank * i * o for i, o in zip(ins, outs))
-    assert plan.describe(-1, 1)["bytes"] == 2.0 * (params + spec.in_features + spec.out_features)
+    elem = dt.itemsize
+    assert plan.describe(-1, 1)["bytes"] == elem * (params + spec.in_features + spec.out_features)
 
 
 def test_module_names_do_not_depend_on_the_checkout_path(monkeypatch):
@@ -68,11 +71,11 @@ def test_module_names_do_not_depend_on_the_checkout_path(monkeypatch):
     assert jit.module_path(shape) != here
 
 
-def test_fp32_and_disabled_jit_keep_the_generic_kernel(monkeypatch):
+def test_disabled_jit_keeps_the_generic_kernel(monkeypatch):
     spec = TRSpec((4, 6, 8), (6, 4, 8), 8)
-    assert not make_plan(spec, torch.float32).has_mfma
     monkeypatch.setenv("TRK_JIT", "0")
-    assert not make_plan(spec, torch.float16).has_mfma
+    for dtype in (torch.float16, torch.float32):
+        assert not make_plan(spec, dtype).has_mfma
 
 
 def test_loader_rejects_other_libraries():

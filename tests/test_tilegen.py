@@ -23,7 +23,7 @@ HAND = [
     tilegen.ShapeDecl("up", (16, 16, 16), (16, 28, 32), 8, "bf16"),
     tilegen.ShapeDecl("down", (16, 28, 32), (16, 16, 16), 16, "bf16"),
 ]
-DT = {"f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16}
+DT = {"f16": _lib.DTYPE_F16, "bf16": _lib.DTYPE_BF16, "f32": _lib.DTYPE_F32}
 
 
 def parse(name: str):
