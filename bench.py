@@ -50,7 +50,7 @@ CASES = [  # (label, input modes, output modes, rank, dtype, init, tokens)
     ("r16", (8, 12, 20), (12, 10, 24), 16, "float16", "per_core", (1, 32)),
     ("llama_up_r8", (16, 16, 16), (16, 28, 32), 8, "bfloat16", "uniform", (1, 8, 32, 128)),
     ("llama_down_r16", (16, 28, 32), (16, 16, 16), 16, "bfloat16", "uniform", (1, 32, 256)),
-    # the reference's CPU-runnable case in fp32 (the generic HIP kernel), the GPU
+    # the reference's CPU-runnable case in fp32 (on fp32 MFMAs), the GPU
     # figure to set beside the CPU baseline, which times the same config
     ("r8_fp32", (8, 12, 20), (12, 10, 24), 8, "float32", "per_core", (1, 8, 32)),
 ]
