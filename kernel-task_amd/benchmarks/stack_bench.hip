@@ -104,7 +104,12 @@ __device__ __forceinline__ void xcd_arrive(unsigned *counter) {
 // one-XCD barrier, wait half. The counter is read with compare-and-swaps that never swap (it
 // never holds 2^32 - 1): they execute in the L2 and return its value, while a plain load may
 // be served a stale L1 line (and the compiler turns an atomic add of 0 into such a load).
-// Then the CU's L1 is invalidated, so the next reads of activations come from the L2.
+// The layer's reads of its input activations then use device-scope loads (ring3_unit's
+// COHERENT_X), which the CU's L1 does not serve, so they see the L2's current lines. (An L1
+// invalidation at workgroup scope, `buffer_inv sc0`, was not enough: outside threadgroup-split
+// mode a workgroup's waves share one L1, so that scope need not touch it, and stale lines of
+// an activation buffer from two layers back were read, 1 run in ~8 giving wrong outputs. The
+// device-scope invalidation, `buffer_inv sc1`, made each barrier cost 11.7 µs.)
 __device__ __forceinline__ void xcd_wait(unsigned *counter, unsigned target, int *err, int spin) {
     if (threadIdx.x == 0) {
         for (int n = 0;;) {
@@ -120,7 +125,6 @@ __device__ __forceinline__ void xcd_wait(unsigned *counter, unsigned target, int
         }
     }
     __syncthreads();
-    asm volatile("buffer_inv sc0" ::: "memory");
 }
 
 // This workgroup's units of one layer. A nonzero target means the previous layer's barrier is
@@ -138,15 +142,20 @@ __device__ __forceinline__ void run_layer(const Layer &lay, const E *in, E *out,
             if (pending) xcd_wait(counter, target, err, spin);
             pending = false;
         };
+        // the one-XCD form reads the activations with device-scope loads (see xcd_wait); the
+        // device-scope barrier of the other form invalidates the CU's L1 itself
+        constexpr bool COHERENT = STACK_XCD != 0;
         if constexpr (PREFETCH) {
-            ring3_unit<C, false>(in, lay.fk, lay.sk, lay.lk, out, T, 0, nullptr, u % G::NBLK,
-                                 u / G::NBLK, pool + G::oFs, pool + G::oSs, pool + G::oLs,
-                                 pool + G::oXs, pool + G::oUb, pool + G::oVb, wait);
+            ring3_unit<C, false, decltype((wait)), false, COHERENT>(
+                in, lay.fk, lay.sk, lay.lk, out, T, 0, nullptr, u % G::NBLK, u / G::NBLK,
+                pool + G::oFs, pool + G::oSs, pool + G::oLs, pool + G::oXs, pool + G::oUb,
+                pool + G::oVb, wait);
         } else {
             wait();
-            ring3_unit<C, false>(in, lay.fk, lay.sk, lay.lk, out, T, 0, nullptr, u % G::NBLK,
-                                 u / G::NBLK, pool + G::oFs, pool + G::oSs, pool + G::oLs,
-                                 pool + G::oXs, pool + G::oUb, pool + G::oVb);
+            ring3_unit<C, false, NoHook, false, COHERENT>(
+                in, lay.fk, lay.sk, lay.lk, out, T, 0, nullptr, u % G::NBLK, u / G::NBLK,
+                pool + G::oFs, pool + G::oSs, pool + G::oLs, pool + G::oXs, pool + G::oUb,
+                pool + G::oVb);
         }
         __syncthreads();  // the next unit reuses the LDS
     }

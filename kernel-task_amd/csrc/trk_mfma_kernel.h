@@ -766,14 +766,38 @@ struct NoHook {
 // hook, when given, is called by every thread once the unit's core-slice loads are in flight
 // and before any load of x, which is then issued after it: a persistent caller's wait for the
 // layer that writes x (the core slices do not depend on it). Without a hook the loads keep
-// the standalone order.
+// the standalone order. COHERENT_X reads x with device-scope loads, which the CU's L1 does not
+// serve: for x written earlier in the same launch by workgroups on other CUs (a persistent
+// caller), whose lines an older read may have left in this CU's L1.
 // Sections of the packed cores one pass of ring3_unit reads.
 template <class E>
 struct CoreSections {
     const E *fk, *sk, *lk;
 };
 
-template <KCfg C, bool EPI, class Hook = NoHook, bool PAIR = false>
+// A load of `T` (4, 8 or 16 bytes) at device scope: relaxed atomic loads of its 4- or 8-byte
+// words (the memory model's device-scope load, which does not use the CU's L1).
+template <class T>
+__device__ __forceinline__ T load_device_scope(const T *p) {
+    static_assert(sizeof(T) % 4 == 0 && sizeof(T) <= 16, "4-, 8- or 16-byte loads");
+    T r;
+    if constexpr (sizeof(T) % 8 == 0) {
+        auto *src = reinterpret_cast<const unsigned long long *>(p);
+        auto *dst = reinterpret_cast<unsigned long long *>(&r);
+#pragma unroll
+        for (int i = 0; i < int(sizeof(T) / 8); ++i)
+            dst[i] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        auto *src = reinterpret_cast<const unsigned *>(p);
+        auto *dst = reinterpret_cast<unsigned *>(&r);
+#pragma unroll
+        for (int i = 0; i < int(sizeof(T) / 4); ++i)
+            dst[i] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return r;
+}
+
+template <KCfg C, bool EPI, class Hook = NoHook, bool PAIR = false, bool COHERENT_X = false>
 __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restrict__ x,
                                            const typename Ops<C.dt>::E *__restrict__ Fk0,
                                            const typename Ops<C.dt>::E *__restrict__ Sk0,
@@ -836,15 +860,25 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
         const int iS = n % G::nSP, t = (n / G::nSP) % G::TT, iL = iL0 + n / (G::nSP * G::TT);
         XV r{};
         if ((G::NXV % LT == 0 || v < G::NXV) && c * G::VX < G::nF && iS < G::nS &&
-            t0 + t < T)
-            r = *reinterpret_cast<const XV *>(x + size_t(t0 + t) * G::IN + iS * G::SXS +
-                                              iL * G::SXL + c * G::VX);
+            t0 + t < T) {
+            const XV *p = reinterpret_cast<const XV *>(x + size_t(t0 + t) * G::IN + iS * G::SXS +
+                                                       iL * G::SXL + c * G::VX);
+            if constexpr (COHERENT_X)
+                r = load_device_scope(p);
+            else
+                r = *p;
+        }
         return r;
     };
-    auto x_scatter_load = [&](int v) TRK_INLINE {       // scatter loader: 8 contiguous x elements
+    auto x_scatter_load = [&](int v) TRK_INLINE {       // scatter loader: one 16-byte x vector
         uint4 r = make_uint4(0u, 0u, 0u, 0u);
-        if (v < G::NXB && t0 + v / (G::IN / G::VPE) < T)
-            r = reinterpret_cast<const uint4 *>(x + size_t(t0) * G::IN)[v];
+        if constexpr (COHERENT_X) {
+            if (v < G::NXB && t0 + v / (G::IN / G::VPE) < T)
+                r = load_device_scope(reinterpret_cast<const uint4 *>(x + size_t(t0) * G::IN) + v);
+        } else {
+            if (v < G::NXB && t0 + v / (G::IN / G::VPE) < T)
+                r = reinterpret_cast<const uint4 *>(x + size_t(t0) * G::IN)[v];
+        }
         return r;
     };
     auto x_scatter_store = [&](int v, uint4 r, int iL0, E *xs) TRK_INLINE {
