@@ -308,9 +308,10 @@ def _cpu_model() -> str:
             f"stepping {fields.get('stepping', '?')})")
 
 
-def traffic_probe(calls: int, case: str = "r8:1") -> None:
+def traffic_probe(calls: int, case: str = "r8:1", variant: str | None = None) -> None:
     """Workload of the rocprofv3 --pmc runs: `calls` launches of one case's kernel (`case` is
-    "label:tokens" of CASES; the headline r8:1 by default), then a plain 512 MiB device copy
+    "label:tokens" of CASES; the headline r8:1 by default; `variant` names another compiled
+    variant of the plan to launch instead of its default), then a plain 512 MiB device copy
     (5 launches; larger than every L2 and the 256 MB MALL, so its reads come from HBM) whose
     counters give the scale factor between counted and actual bytes."""
     import torch
@@ -326,6 +327,11 @@ def traffic_probe(calls: int, case: str = "r8:1") -> None:
     spec = TRSpec(ins, outs, rank)
     cores = make_cores(spec, device="cuda", dtype=dtype, seed=0, init=init)
     run = prepare_optimized(cores, spec)
+    if variant is not None:
+        names = [v["name"] for v in run.variants(T)]
+        if variant not in names:
+            raise SystemExit(f"--probe-variant {variant!r} is not one of {names}")
+        run.plan.set_variant(1, 1 << 30, names.index(variant))
     x = torch.randn(T, spec.in_features, generator=torch.Generator(device="cuda").manual_seed(1),
                     device="cuda", dtype=dtype)
     for _ in range(calls):
@@ -409,13 +415,15 @@ def main() -> int:
                     help="only run the workload of the counter (rocprofv3 --pmc) runs")
     ap.add_argument("--probe-case", default="r8:1", metavar="LABEL:TOKENS",
                     help="case of the --traffic-probe workload (default r8:1, the headline)")
+    ap.add_argument("--probe-variant", default=None, metavar="NAME",
+                    help="variant the --traffic-probe workload launches (default: the plan's)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         return 2
     if args.traffic_probe:
-        traffic_probe(args.traffic_probe, args.probe_case)
+        traffic_probe(args.traffic_probe, args.probe_case, args.probe_variant)
         return 0
     if args.runtime_default_child:
         return runtime_default_child(args.steps, args.warmup)

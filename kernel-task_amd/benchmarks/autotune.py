@@ -21,7 +21,8 @@ count, src/factorized_inference/v3g_tuned.py:4-17). Timing, median of three bloc
   T=128: a graph put two tiles 1 % apart, eager calls 7 % apart the other way).
 
 Every variant's output is checked against the shape's default variant before it may win (bitwise equality
-is not expected across tiles: the stage-3 summation order differs).
+is not expected across tiles: the stage-3 summation order differs). Timings within 1 % count
+as equal, and then the tile on the fewest XCDs wins (Tile.XL).
 
 Candidates span every chain order the generator searches (tilegen.search_orders); each
 range records its winner's order. Token counts measured: 1, 2, 4, 8, 16, 32, 64, 128, 256. The winner at T serves the range
@@ -92,6 +93,21 @@ def eager_us(fn, calls: int, blocks: int = 3) -> float:
 
 
 EAGER_FROM_US = 12.0  # tiles this slow (graph-timed) are re-timed with eager calls
+PLACEMENT_TIE = 0.01  # timings this close count as equal: the fewer XCDs win
+
+
+def xcds(tile: tilegen.Tile) -> int:
+    """XCDs a tile's launch runs on (Tile.XL; 0 means all 8)."""
+    return tile.XL or 8
+
+
+def winner(row: dict[str, float], tiles: dict) -> str:
+    """The fastest tile of one token count; among tiles within PLACEMENT_TIE of it, the one
+    on the fewest XCDs (less HBM traffic and L2 write-back for the same latency, and the
+    other XCDs stay free for concurrent work)."""
+    best = min(row, key=row.get)
+    close = [n for n in row if row[n] <= row[best] * (1 + PLACEMENT_TIE)]
+    return min(close, key=lambda n: (xcds(tiles[n][1]), row[n]))
 
 
 def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
@@ -138,7 +154,7 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
                 us = eager_us(fn, calls)
             row[names[i]] = us
         measured[T] = row
-        best = min(row, key=row.get)
+        best = winner(row, tiles)
         print(f"{shape.key} T={T:4d}: " + "  ".join(
             f"{n} {us:7.2f}{'*' if n == best else ''}" for n, us in sorted(row.items())),
             flush=True)
@@ -151,7 +167,7 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
     done = sorted(measured)
     for k, T in enumerate(done):
         row = measured[T]
-        best = min(row, key=row.get)
+        best = winner(row, tiles)
         hi = (1 << 30) if k == len(done) - 1 else T
         if ranges and ranges[-1]["name"] == best:
             ranges[-1]["t_max"] = hi

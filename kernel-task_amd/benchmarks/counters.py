@@ -7,6 +7,9 @@ kernel traces.
     python kernel-task_amd/benchmarks/counters.py means DIR [DIR ...]
     # back-to-back blocks of one kernel in a --kernel-trace run (e.g. bench.py's timed block)
     python kernel-task_amd/benchmarks/counters.py blocks TRACE.csv --kernel REGEX [--grid N]
+    # durations per (tensor-ring kernel, grid) in a --kernel-trace run: one kernel serves
+    # several token counts (grids), which rocprofv3's --stats summary lumps together
+    python kernel-task_amd/benchmarks/counters.py grids TRACE.csv [--out FILE.json]
 
 A probe run (bench.py --traffic-probe CALLS) launches one tensor-ring kernel CALLS times and
 then copies a 512 MiB buffer 5 times. The copy is larger than every L2 and the 256 MB MALL,
@@ -124,6 +127,31 @@ def blocks(trace: Path, pattern: str, grid: int | None = None, max_gap_us: float
     return out
 
 
+def grids(trace: Path) -> list[dict]:
+    """Per (tensor-ring or empty kernel, grid in workgroups x * y): dispatches and mean, min
+    and median duration in us, most dispatched first."""
+    acc: dict = defaultdict(list)
+    with open(trace, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            label = kernel_label(name) or ("empty" if "empty" in name else None)
+            if label is None:
+                continue
+            if label == "empty":
+                label = name.replace("(anonymous namespace)::", "").split("(")[0].split("::")[-1]
+            wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"])
+            g = (int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]),
+                 int(r["Grid_Size_Y"]) // int(r["Workgroup_Size_Y"]))
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            acc[(label, g, wg)].append(d)
+    out = []
+    for (label, g, wg), d in acc.items():
+        d.sort()
+        out.append({"kernel": label, "grid": list(g), "threads": wg, "dispatches": len(d),
+                    "mean_us": sum(d) / len(d), "min_us": d[0], "median_us": d[len(d) // 2]})
+    return sorted(out, key=lambda r: -r["dispatches"])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -140,7 +168,17 @@ def main() -> int:
     bp.add_argument("--kernel", required=True, help="regular expression on the kernel name")
     bp.add_argument("--grid", type=int, default=None, help="grid size in threads (x * y)")
     bp.add_argument("--max-gap-us", type=float, default=30.0)
+    gp = sub.add_parser("grids")
+    gp.add_argument("trace", type=Path)
+    gp.add_argument("--out", type=Path)
     args = ap.parse_args()
+    if args.cmd == "grids":
+        text = json.dumps(grids(args.trace), indent=1) + "\n"
+        if args.out:
+            args.out.write_text(text)
+        else:
+            print(text, end="")
+        return 0
     if args.cmd == "blocks":
         print(json.dumps(blocks(args.trace, args.kernel, args.grid, args.max_gap_us), indent=1))
         return 0

@@ -45,7 +45,7 @@ void grid_of(const Plan &p, const Variant &v, int tokens, int grid[3]) {
     } else {
         const int TT = v.tile[0], FC = v.tile[1], SC = v.tile[2], LC = v.tile[3];
         grid[0] = ((c.oF + FC - 1) / FC) * ((c.oS + SC - 1) / SC) * ((c.oL + LC - 1) / LC) *
-                  (v.xcd_local ? 8 : 1);
+                  (v.xcd_local ? 8 / v.xcd_local : 1);
         grid[1] = std::max(1, (tokens + TT - 1) / TT);
         grid[2] = 1;
     }

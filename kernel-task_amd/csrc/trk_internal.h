@@ -67,7 +67,7 @@ struct Variant {
     int block;       // threads per workgroup
     int lds_bytes;   // dynamic LDS per workgroup
     int t_min, t_max;
-    int xcd_local;   // 1: the launch's work runs on XCD 0 only (KCfg::XL; grid x 8)
+    int xcd_local;   // XCDs the launch's work runs on: 0 = all 8; 1, 2, 4 (KCfg::XL; grid x 8/XL)
     char name[64];
     LaunchFn launch;
     LaunchPairFn launch_pair;  // fused SwiGLU gate/up launcher, or null

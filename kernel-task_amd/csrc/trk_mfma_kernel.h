@@ -152,11 +152,12 @@ struct KCfg {
                              // consecutive steps share one barrier interval; 0: one buffer
     int S1;                  // WIDE stage 1: row tiles per wave (the waves split the columns
                              // NW * S1 / M1T ways); 0: the default split (below)
-    int XL;                  // 1: XCD-local launch. The grid is 8x larger and the dispatcher
+    int XL;                  // XCDs the launch's work runs on: 0 = all 8; 1, 2 or 4 = the
+                             // first XL. The grid is 8 / XL times larger and the dispatcher
                              // deals workgroups to the 8 XCDs round-robin; those dealt to XCDs
-                             // 1-7 exit at once, so every working workgroup shares XCD 0's L2:
-                             // each core slice crosses from HBM once and every cache line of y
-                             // is written back by one L2 (fewer CUs, for small launches)
+                             // XL..7 exit at once, so the working ones share XL L2s: each core
+                             // slice crosses from HBM at most XL times and a cache line of y is
+                             // written back by at most XL L2s (for launches that fit XL x 32 CUs)
 };
 
 // K orders of the packed second- and last-core sections a variant reads (its chain's layout):
@@ -367,7 +368,8 @@ struct Geo {
 
     static_assert(R % 8 == 0 && (R & (R - 1)) == 0, "MFMA variants need a power-of-two rank >= 8");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
-    static_assert(C.XL == 0 || C.XL == 1, "XL is 0 or 1");
+    static_assert(C.XL == 0 || C.XL == 1 || C.XL == 2 || C.XL == 4, "XL is 0, 1, 2 or 4");
+    static_assert(C.XL == 0 || NBLK % C.XL == 0, "XL must divide the workgroups of a token tile");
     static_assert(C.WIDE >= 0 && C.WIDE <= NW && (C.WIDE == 0 || NW % C.WIDE == 0),
                   "WIDE is 0 or divides the waves");
     static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
@@ -1328,6 +1330,29 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     }
 }
 
+// The work unit (tile index within a token tile) of workgroup column `bx`, or -1 for a
+// workgroup that has no work. Workgroups are dealt round-robin to the 8 XCDs, each with its
+// own L2 (with a multiple of 8 columns, the linear workgroup index has the residue of bx
+// modulo 8). A launch on XL XCDs keeps the workgroups dealt to XCDs 0..XL-1. The units are
+// renumbered so that consecutive ones (the same first-core digit f, hence the same Fs slice)
+// share an XCD.
+template <KCfg C>
+__device__ __forceinline__ int unit_of_workgroup(int bx) {
+    using G = Geo<C>;
+    if constexpr (C.XL) {
+        if (bx % 8 >= C.XL) return -1;
+        const int w = (bx / 8) * C.XL + bx % 8;  // XCD w % XL, 0 <= w < NBLK
+        return (w % C.XL) * (G::NBLK / C.XL) + w / C.XL;
+    } else if constexpr (G::NBLK % 8 == 0) {
+        return (bx % 8) * (G::NBLK / 8) + bx / 8;
+    }
+    return bx;
+}
+
+inline const char *xl_tag(int xl) {
+    return xl == 1 ? "_xl" : xl == 2 ? "_x2" : xl == 4 ? "_x4" : "";
+}
+
 // EPI: false compiles the plain store of the plan's dtype only (epi_mode is ignored); true
 // compiles every epilogue, chosen at run time by epi_mode. Two instantiations keep the plain
 // path's code exactly as it is without epilogues (measured: a run-time branch in its store
@@ -1354,17 +1379,8 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
     __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
 
-    // Workgroups are dealt round-robin to the 8 XCDs, each with its own L2. Renumber them so
-    // that consecutive tiles (same first-core digit f, hence the same Fs slice) share an XCD;
-    // an XCD-local launch keeps only the workgroups dealt to XCD 0 (blockIdx.x % 8 == 0: with
-    // 8 * NBLK columns the linear workgroup index has the same residue modulo 8).
-    int b = blockIdx.x;
-    if constexpr (C.XL) {
-        if (b % 8 != 0) return;  // uniform per workgroup, before any barrier or access
-        b /= 8;
-    } else if constexpr (G::NBLK % 8 == 0) {
-        b = (b % 8) * (G::NBLK / 8) + b / 8;
-    }
+    const int b = unit_of_workgroup<C>(blockIdx.x);
+    if (b < 0) return;  // uniform per workgroup, before any barrier or access
     ring3_unit<C, EPI>(x, Fk, Sk, Lk, y, T, epi_mode, aux, b, blockIdx.y, Fs, Ss, Ls, Xs, Ub, Vb);
 }
 
@@ -1386,7 +1402,7 @@ int launch_mfma(const Plan &plan, const Variant &v, const void *packed, const vo
     const size_t aux_elem = (epi.mode & kAuxF32) ? 4 : sizeof(E);
     for (int t0 = 0; t0 < tokens; t0 += per_launch) {
         const int n = tokens - t0 < per_launch ? tokens - t0 : per_launch;
-        const dim3 grid(G::NFC * G::NSC * G::NLC * (C.XL ? 8 : 1), (n + G::TT - 1) / G::TT);
+        const dim3 grid(G::NFC * G::NSC * G::NLC * (C.XL ? 8 / C.XL : 1), (n + G::TT - 1) / G::TT);
         const E *xe = static_cast<const E *>(x) + size_t(t0) * G::IN;
         void *yc = static_cast<char *>(y) + size_t(t0) * G::OUT * y_elem;
         const void *ac =
@@ -1419,13 +1435,8 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     __shared__ __attribute__((aligned(16))) E Xs[G::NBUF * G::szXs];
     __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
     __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
-    int b = blockIdx.x;
-    if constexpr (C.XL) {
-        if (b % 8 != 0) return;
-        b /= 8;
-    } else if constexpr (G::NBLK % 8 == 0) {
-        b = (b % 8) * (G::NBLK / 8) + b / 8;
-    }
+    const int b = unit_of_workgroup<C>(blockIdx.x);
+    if (b < 0) return;
     const CoreSections<E> up{reinterpret_cast<const E *>(packed_u + offF),
                              reinterpret_cast<const E *>(packed_u + offS),
                              reinterpret_cast<const E *>(packed_u + offL)};
@@ -1446,7 +1457,7 @@ int launch_pair(const Plan &plan, const Variant &v, const void *packed_g, const 
     const int per_launch = kMaxTiles * G::TT;
     for (int t0 = 0; t0 < tokens; t0 += per_launch) {
         const int n = tokens - t0 < per_launch ? tokens - t0 : per_launch;
-        const dim3 grid(G::NFC * G::NSC * G::NLC * (C.XL ? 8 : 1), (n + G::TT - 1) / G::TT);
+        const dim3 grid(G::NFC * G::NSC * G::NLC * (C.XL ? 8 / C.XL : 1), (n + G::TT - 1) / G::TT);
         hipLaunchKernelGGL((ring3_pair_kernel<C>), grid, dim3(G::NT), 0, stream,
                            static_cast<const E *>(x) + size_t(t0) * G::IN,
                            static_cast<const char *>(packed_g), static_cast<const char *>(packed_u),
@@ -1518,12 +1529,12 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
             std::snprintf(v.name, sizeof(v.name),
                           "ring3_mfma_wide%d%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
                           k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "",
-                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, k.XL ? "_xl" : "", k.F,
+                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, xl_tag(k.XL), k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         } else {
             std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
                           k.NW == 8 ? "_w8" : "", k.PIPE == 2 ? "_p2" : k.PIPE ? "_p" : "",
-                          k.XL ? "_xl" : "", k.F,
+                          xl_tag(k.XL), k.F,
                           k.S, k.L, k.TT, k.FC,
                           k.SC, k.LC, k.IC, k.KS3, k.NACC);
         }

@@ -95,7 +95,7 @@ class Tile:
     PIPE: int = 0  # 1: double-buffered slices, two barriers per step; 2: also double-buffered
     #                stage results, three steps' stages in one barrier interval
     S1: int = 0    # WIDE stage-1 row tiles per wave (0: the kernel's default split)
-    XL: int = 0    # 1: XCD-local launch (all work on XCD 0, one L2; KCfg::XL)
+    XL: int = 0    # XCDs the launch's work runs on: 0 = all 8; 1, 2 or 4 (KCfg::XL)
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
@@ -329,6 +329,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         fa = BM1 * (KF // 32 * v8 + tail(KF))
         sa = BM2 * (K2 // 16) * v8 if W32 else BM2 * (K2 // 32 * v8 + tail(K2))
         g["slice_vgprs"] = fa + sa
+    nblk = g["NBLK"]
     checks = [
         (R % 8 == 0 and R & (R - 1) == 0, "rank must be a power of two >= 8"),
         (NW in (4, 8), "4 or 8 waves"),
@@ -344,7 +345,8 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (c.nL % t.IC == 0, "IC must divide the last core's input mode"),
         (t.PIPE in (0, 1, 2) and (t.PIPE == 0 or c.nL // t.IC > 1), "a pipelined tile needs two steps"),
         (t.S1 == 0 or (wide and WM1 > 0 and NW % WM1 == 0), "S1 must split the stage-1 rows"),
-        (t.XL in (0, 1), "XL is 0 or 1"),
+        (t.XL in (0, 1, 2, 4), "XL is 0, 1, 2 or 4"),
+        (t.XL == 0 or nblk % t.XL == 0, "XL must divide the workgroups of a token tile"),
         (c.xrow or c.IN % (16 // eb) == 0, "scatter loader reads x rows in 16-byte vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= N2R * P2 * eb, "stage-3 reduction does not fit in Ub"),
@@ -484,6 +486,18 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
                     p = replace(t, PIPE=pipe)
                     if not geometry(shape, order, p)["reject"] and p not in out.values():
                         out[name + tag] = p
+        # single-token tiles placed on 1, 2 or 4 XCDs where each workgroup of one token tile
+        # still gets a CU of its own (32 per XCD): fewer L2s fetch the core slices and write
+        # back the lines of y, at the same per-workgroup latency
+        for name, t in list(out.items()):
+            if t.TT != 1 or t.WIDE or t.XL:
+                continue
+            nblk = geometry(shape, order, t)["NBLK"]
+            for xl in (1, 2, 4):
+                p = replace(t, XL=xl)
+                if (nblk <= 32 * xl and not geometry(shape, order, p)["reject"]
+                        and p not in out.values()):
+                    out[name + ("_xl" if xl == 1 else f"_x{xl}")] = p
     if not any(n.startswith("wide") for n in out):
         # no register-resident tile within the budget (a long stage-2 K): offer the smallest
         # over-budget one, which may spill a few registers; the autotuner decides
@@ -495,7 +509,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
 
 
 _VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?(?:_s(\d+))?|(_w8)?(_p2?)?)"
-                           r"(_xl)?<(\d)(\d)(\d),"
+                           r"(_xl|_x[24])?<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -511,7 +525,7 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     pipe = 2 if pipe_tag.endswith("2") else 1 if pipe_tag else 0
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
                        8 if (m.group(3) or m.group(6)) else 4, pipe, int(m.group(5) or 0),
-                       1 if m.group(8) else 0)
+                       {None: 0, "_xl": 1, "_x2": 2, "_x4": 4}[m.group(8)])
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:

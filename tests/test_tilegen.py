@@ -49,11 +49,15 @@ def test_variant_names_parse_back_to_their_tiles():
         1, 1, 10, 12, 8, 4, 1, 0, 16, 8, XL=1)
     assert parse("ring3_mfma_wide8x32w8p_s4_xl<210,4,1,10,12,2,2,1>")[1] == tilegen.Tile(
         4, 1, 10, 12, 2, 2, 1, 8, 32, 8, 1, 4, 1)
+    assert parse("ring3_mfma_x4<210,1,1,2,12,8,4,1>")[1] == tilegen.Tile(
+        1, 1, 2, 12, 8, 4, 1, XL=4)
+    assert parse("ring3_mfma_p_x2<210,1,1,5,12,8,1,2>")[1] == tilegen.Tile(
+        1, 1, 5, 12, 8, 1, 2, PIPE=1, XL=2)
     with pytest.raises(ValueError):
         parse("ring3_generic<012,rc=8>")
 
 
-def test_xcd_local_tiles_emit_every_trailing_argument():
+def test_xcd_placed_tiles_emit_every_trailing_argument():
     # XL is the last argument of tile(shape, ...), so an XCD-local tile spells out the
     # defaults before it
     assert tilegen.Tile(1, 1, 10, 12, 8, 4, 1, 0, 16, 8, XL=1).args() == \
@@ -61,13 +65,21 @@ def test_xcd_local_tiles_emit_every_trailing_argument():
     assert tilegen.Tile(1, 1, 2, 12, 8, 4, 1).args() == "1, 1, 2, 12, 8, 4, 1"
     # the headline shape's table carries an XCD-local tile, index-only, beside its winners
     shape = tilegen.BASELINE[0]
-    xl = [(n, t, lo, hi) for n, _, t, lo, hi in tilegen.table(shape) if t.XL]
+    xl = [(n, t, lo, hi) for n, _, t, lo, hi in tilegen.table(shape) if t.XL == 1]
     assert xl and all((lo, hi) == (0, 0) for *_, lo, hi in xl)
-    # and the extended search offers XCD-local single-token tiles
-    assert any(t.XL for t in tilegen.candidates(shape, extended=True).values())
+    # and the extended search offers single-token tiles on 1, 2 and 4 XCDs; those on 2 and 4
+    # only where a token tile's workgroups fit those XCDs' CUs
+    placed = [(o, t) for o, t in tilegen.search_candidates(shape, extended=True).values() if t.XL]
+    assert {t.XL for _, t in placed} == {1, 2, 4}
+    for o, t in placed:
+        nblk = tilegen.geometry(shape, o, t)["NBLK"]
+        assert t.TT == 1 and nblk % t.XL == 0 and (t.XL == 1 or nblk <= 32 * t.XL)
     plan = _lib.Plan(shape.ins, shape.outs, shape.rank, DT[shape.dtype])
     v = next(v for v in plan.variants(1) if "_xl<" in v["name"])
     assert v["grid"][0] == 8 * 24 and v["t_min"] == 0
+    # the tuned single-token winner runs on 4 XCDs: 120 working workgroups in a grid of 240
+    v = plan.describe(-1, 1)
+    assert "_x4<" in v["name"] and v["grid"][0] == 2 * 120
 
 
 @pytest.mark.parametrize("shape", HAND + tilegen.DECLARED, ids=lambda s: s.key)
