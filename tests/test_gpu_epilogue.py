@@ -272,7 +272,7 @@ def test_forward_swiglu(shape, rank, tokens):
     if tokens is None:
         tokens = sorted({v["t_min"] for v in gate.variants()
                          if v["kind"] == "mfma" and 0 < v["t_min"] <= 256})
-        assert len(tokens) >= 6
+        assert len(tokens) >= 4  # single-token, mid-size and register-resident tiles
     for T in tokens:
         announce(test="fused gate/up", shape=shape, rank=rank, tokens=T,
                  variant=gate.selected(T)["name"])
