@@ -20,9 +20,12 @@ shapes) gets a generated table:
 The extended search (--extended, the autotuner's input) widens step 2: further chain orders
 within 15 % of the least padded work, 1-8 tokens per workgroup in every family, quarter and
 eighth second-core tiles, single-token tiles without the stage-3 wave reduction, more
-last-core inputs per step, a 4-row-group register-resident family on 8 waves, the two
-pipelined main loops (PIPE 1 and 2) of every multi-step tile, and larger stage-1 row groups
-(S1) of the previous winners.
+last-core inputs per step, a 4-row-group register-resident family on 8 waves, one token
+(and one token with two first-core digits) per register-resident workgroup, the two
+pipelined main loops (PIPE 1 and 2) of every multi-step tile, single-token tiles placed on
+1, 2 or 4 XCDs, larger stage-1 row groups (S1) of the previous winners, and the neighbours
+of the previous register-resident winners (tokens, first-core digits, main loop, S1 and
+stage-3 split varied together).
 
 Role of the reference's V3G generators (tools/gen_v3g_tilings.py, tools/gen_v3g_tuned.py,
 src/factorized_inference/v3g_tuned.py:4-17): a compiled variant list for the Qwen3.8-27B
@@ -580,6 +583,24 @@ def s1_variants(shape: ShapeDecl, order: tuple, t: Tile) -> dict[str, Tile]:
     return out
 
 
+def neighbours(shape: ShapeDecl, order: tuple, t: Tile) -> dict[str, Tile]:
+    """Local refinements of a register-resident tile that won a range of 5 tokens or more:
+    1-4 tokens and 1-2 first-core digits per workgroup, each main loop, each stage-1 row
+    group and two stage-3 splits, every one the kernel accepts (the autotuner's second pass;
+    it gained 3-6 % at 3-256 tokens on the BASELINE shapes after the first)."""
+    out = {}
+    if not t.WIDE:
+        return out
+    for tt, fc in ((1, 1), (1, 2), (2, 1), (2, 2), (4, 1)):
+        for pipe in (0, 1, 2):
+            for s1 in (0, 2, 4, 8):
+                for ks3, nacc in ((t.KS3, t.NACC), (1, 2), (2, 1)):
+                    v = replace(t, TT=tt, FC=fc, PIPE=pipe, S1=s1, KS3=ks3, NACC=nacc)
+                    if v != t and v not in out.values() and not geometry(shape, order, v)["reject"]:
+                        out[f"~t{tt}f{fc}p{pipe}s{s1}k{ks3}n{nacc}"] = v
+    return out
+
+
 def search_candidates(shape: ShapeDecl, extended: bool = False) -> dict[str, tuple[tuple, Tile]]:
     """name -> (order, tile) over every searched order; tiles of an order other than the
     shape's own carry the suffix @FSL in their names."""
@@ -616,7 +637,8 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
     ranges = rule_ranges([n for n, (o, _) in cands.items() if o == first])
     if all_candidates and shape.key in tuned:
         # the previous winners stay candidates, so a new search never loses a tile it had;
-        # an extended search also tries their larger stage-1 row groups (a local refinement)
+        # an extended search also tries their larger stage-1 row groups and, for the
+        # register-resident winners of 5 tokens or more, their neighbours (a local refinement)
         entry = tuned[shape.key]
         for r in entry["ranges"] + entry.get("extra", []):
             order = tuple(r.get("order", entry["order"]))
@@ -632,6 +654,9 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
             if extended:
                 found += [(base + suffix + tag, v)
                           for suffix, v in s1_variants(shape, order, tile).items()]
+                if r.get("t_min", 0) >= 5:
+                    found += [(base[:40] + suffix + tag, v)
+                              for suffix, v in neighbours(shape, order, tile).items()]
             for n, t in found:
                 if (order, t) not in cands.values():
                     cands[n] = (order, t)
