@@ -52,3 +52,49 @@ def test_means_ignore_other_kernels(tmp_path):
     m = counters.means(tmp_path / "s")
     assert set(m) == {counters.probed_kernel(m), "copy"}
     assert m[counters.probed_kernel(m)]["SQ_WAVES"] == {"dispatches": 3, "mean": 1536.0}
+
+
+def write_trace(path: Path, rows):
+    """A --kernel-trace csv: rows of (name, grid_x_threads, grid_y, wg_threads, start, end)."""
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Workgroup_Size_X",
+                    "Workgroup_Size_Y", "Grid_Size_X", "Grid_Size_Y"])
+        for name, gx, gy, wg, s, e in rows:
+            w.writerow([name, s, e, wg, 1, gx, gy])
+
+
+def test_grids_split_one_kernel_by_launch_shape(tmp_path):
+    # one kernel at two token counts (grids 240 x 1 and 240 x 16 workgroups), an empty
+    # kernel, and a library kernel that is not summarized
+    empty = "trk::(anonymous namespace)::ring3_empty_args_kernel(void const*)"
+    rows = [(RING, 240 * 256, 1, 256, 0, 3000), (RING, 240 * 256, 1, 256, 5000, 7000),
+            (RING, 240 * 256, 16, 256, 9000, 19000), (empty, 64, 1, 64, 20000, 21500),
+            ("Cijk_Alik_Bljk_HHS", 64, 1, 64, 22000, 30000)]
+    write_trace(tmp_path / "t.csv", rows)
+    g = {(r["kernel"], tuple(r["grid"])): r for r in counters.grids(tmp_path / "t.csv")}
+    ring = counters.kernel_label(RING)
+    assert set(g) == {(ring, (240, 1)), (ring, (240, 16)), ("ring3_empty_args_kernel", (1, 1))}
+    one = g[(ring, (240, 1))]
+    assert one["dispatches"] == 2 and one["mean_us"] == pytest.approx(2.5)
+    assert one["min_us"] == pytest.approx(2.0) and one["threads"] == 256
+    assert g[(ring, (240, 16))]["mean_us"] == pytest.approx(10.0)
+    assert g[("ring3_empty_args_kernel", (1, 1))]["mean_us"] == pytest.approx(1.5)
+
+
+def test_blocks_split_at_gaps(tmp_path):
+    # 12 back-to-back dispatches, a 100 us gap, 12 more, then 3 isolated ones (too few)
+    rows, t = [], 0
+    for run in (12, 12):
+        for _ in range(run):
+            rows.append((RING, 30720, 1, 256, t, t + 3000))
+            t += 3500
+        t += 100000
+    for _ in range(3):
+        rows.append((RING, 30720, 1, 256, t, t + 3000))
+        t += 200000
+    write_trace(tmp_path / "t.csv", rows)
+    b = counters.blocks(tmp_path / "t.csv", r"KCfg\{0, 2, 1, 0", grid=30720)
+    assert [r["dispatches"] for r in b] == [12, 12]
+    assert b[0]["mean_us"] == pytest.approx(3.0) and b[1]["start_us"] > b[0]["start_us"]
+    assert counters.blocks(tmp_path / "t.csv", r"KCfg", grid=61440) == []
