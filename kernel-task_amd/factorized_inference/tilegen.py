@@ -429,6 +429,19 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
         t = wide_tile(wide, nw, WIDE_VGPR_BUDGET[nw])
         if t is not None and t not in out.values():
             out[f"wide{wide}x32" + ("w8" if nw == 8 else "")] = t
+    # one token per register-resident workgroup, twice the base tile's last-core inputs per
+    # step where they fit, pipelined when it takes several steps: the family that won 5-64
+    # tokens on every tuned BASELINE shape (the untuned rule's pick there)
+    base = out.get("wide8x32w8")
+    if base is not None:
+        for ic in (2 * base.IC, base.IC):
+            if ic > c.nL or c.nL % ic:
+                continue
+            t = Tile(1, 1, base.SC, LC, ic, 1, 2, base.WIDE, 32, base.NW,
+                     1 if cdiv(c.nL, ic) > 1 else 0)
+            if not geometry(shape, order, t)["reject"] and t not in out.values():
+                out["wide8x32w8_t1"] = t
+                break
     if extended:
         # XCD-local single-token tiles (every workgroup on one XCD: one L2 fetches each core
         # slice once and owns every line of y). Few workgroups read the replicated last-core
@@ -563,8 +576,11 @@ def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
     original = {n.removesuffix("_relaxed"): n for n in names}
     names = list(original)
     for name, lo, hi in ((pick(*t1, "mid_half", "mid_all", "wide4x32", "wide8x32w8"), 1, 1),
-                         (pick("mid_half", "mid_all", "wide4x32", "wide8x32w8", *t1), 2, 16),
-                         (pick("mid_all", "mid_half", "wide4x32", "wide8x32w8", *t1), 17, 64),
+                         (pick("mid_half", "mid_all", "wide4x32", "wide8x32w8", *t1), 2, 4),
+                         (pick("wide8x32w8_t1", "mid_half", "mid_all", "wide4x32", "wide8x32w8",
+                               *t1), 5, 16),
+                         (pick("wide8x32w8_t1", "mid_all", "mid_half", "wide4x32", "wide8x32w8",
+                               *t1), 17, 64),
                          (pick("wide8x32w8", "wide4x32", "mid_all", "mid_half", *t1), 65,
                           1 << 30)):
         if name is None:
