@@ -167,18 +167,22 @@ __device__ __forceinline__ void run_layer(const Layer &lay, const E *in, E *out,
 template <bool WORK, bool PREFETCH>
 __global__ void __launch_bounds__(NT)
     stack_kernel(const E *x, E *act0, E *act1, E *y, const Layer *layers, int L, int T,
-                 unsigned *counter, unsigned base, int *err, int spin, unsigned *xcc) {
+                 unsigned *counter, unsigned base, int *err, int spin, unsigned *xcc, int xcd) {
     __shared__ __attribute__((aligned(16))) E pool[POOL];
     int wg = blockIdx.x;
     if constexpr (STACK_XCD) {
-        if (wg % 8 != 0) return;  // dealt to XCDs 1-7
-        wg /= 8;
         // the XCD this workgroup runs on (hardware register XCC_ID, bits 3:0): the host
-        // checks that the dealing put every working workgroup on one XCD, which the L2
-        // barrier assumes
+        // checks that every working workgroup ran on one XCD, which the L2 barrier assumes
         unsigned id;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(id));
-        if (threadIdx.x == 0) xcc[wg] = id & 0xfu;
+        id &= 0xfu;
+        // xcd < 0: the workgroups of residue 0 modulo 8 work (one launch at a time, dealt from
+        // XCD 0). xcd >= 0: those running on XCD `xcd` work, for launches side by side whose
+        // dealing starts at different XCDs; round-robin dealing puts one residue class
+        // modulo 8 on each XCD, so wg / 8 still numbers them 0..NWG-1
+        if (xcd < 0 ? wg % 8 != 0 : int(id) != xcd) return;
+        wg /= 8;
+        if (threadIdx.x == 0) xcc[wg] = id;
     }
     for (int l = 0; l < L; ++l) {
         const E *in = l == 0 ? x : ((l - 1) & 1 ? act1 : act0);
@@ -294,8 +298,9 @@ int main(int argc, char **argv) {
         }
     };
     auto stack = [&](int L, bool work, bool prefetch) {
-        int Ti = T, Li = L, spini = spin;
-        void *args[] = {&x, &a0, &a1, &y, &dlayers, &Li, &Ti, &counter, &base, &err, &spini, &xcc};
+        int Ti = T, Li = L, spini = spin, xcd0 = -1;
+        void *args[] = {&x, &a0, &a1, &y, &dlayers, &Li, &Ti, &counter, &base, &err, &spini, &xcc,
+                        &xcd0};
         const void *fn = work ? (prefetch ? (const void *)stack_kernel<true, true>
                                           : (const void *)stack_kernel<true, false>)
                               : (const void *)stack_kernel<false, false>;
@@ -321,6 +326,119 @@ int main(int argc, char **argv) {
         std::sort(t.begin(), t.end());
         return t[2];
     };
+#if STACK_XCD
+    if (const char *par = std::getenv("STACK_PAR")) {
+        // P independent stacks at once, stack k on XCD k (P sequences through one model, each
+        // confined to its own XCD's L2), against one stack alone and against the same tiles
+        // launched per layer for a batch of the P tokens. Plain launches: a stack whose
+        // workgroups were not all resident at once would end its barriers at the spin bound
+        // and report it.
+        const int P = std::atoi(par);
+        if (P < 1 || P > 8 || T != 1) {
+            std::fprintf(stderr, "STACK_PAR wants 1..8 stacks at T=1\n");
+            return 2;
+        }
+        std::vector<hipStream_t> st(P);
+        std::vector<hipEvent_t> ek(P);
+        std::vector<E *> pa0(P), pa1(P), py(P);
+        std::vector<unsigned *> pcnt(P), pxcc(P);
+        std::vector<int *> perr(P);
+        std::vector<unsigned> pbase(P, 0u);
+        for (int k = 0; k < P; ++k) {
+            CHECK(hipStreamCreate(&st[k]));
+            CHECK(hipEventCreateWithFlags(&ek[k], hipEventDisableTiming));
+            for (E **q : {&pa0[k], &pa1[k], &py[k]}) CHECK(hipMalloc(q, MAXF * sizeof(E)));
+            CHECK(hipMalloc(&pcnt[k], sizeof(unsigned)));
+            CHECK(hipMalloc(&perr[k], sizeof(int)));
+            CHECK(hipMalloc(&pxcc[k], sizeof(unsigned) * NWG));
+            CHECK(hipMemset(pcnt[k], 0, sizeof(unsigned)));
+            CHECK(hipMemset(perr[k], 0, sizeof(int)));
+        }
+        E *xb, *c0, *c1, *yb;  // the batch: x's row P times
+        CHECK(hipMalloc(&xb, size_t(P) * 1920 * sizeof(E)));
+        for (int k = 0; k < P; ++k)
+            CHECK(hipMemcpy(xb + size_t(k) * 1920, x, 1920 * sizeof(E), hipMemcpyDeviceToDevice));
+        for (E **q : {&c0, &c1, &yb}) CHECK(hipMalloc(q, size_t(P) * MAXF * sizeof(E)));
+        hipEvent_t ej;
+        CHECK(hipEventCreateWithFlags(&ej, hipEventDisableTiming));
+        auto launch_k = [&](int k, int L, hipStream_t s) {
+            int Ti = 1, Li = L, spini = spin, xk = k;
+            void *args[] = {&x, &pa0[k], &pa1[k], &py[k], &dlayers, &Li, &Ti, &pcnt[k], &pbase[k],
+                            &perr[k], &spini, &pxcc[k], &xk};
+            CHECK(hipLaunchKernel((const void *)stack_kernel<true, true>, dim3(8 * NWG), dim3(NT),
+                                  args, 0, s));
+            pbase[k] += unsigned(L - 1) * NWG;
+        };
+        auto all = [&](int L) {  // the P stacks side by side, joined on the null stream
+            CHECK(hipEventRecord(ej, nullptr));
+            for (int k = 0; k < P; ++k) {
+                CHECK(hipStreamWaitEvent(st[k], ej, 0));
+                launch_k(k, L, st[k]);
+                CHECK(hipEventRecord(ek[k], st[k]));
+            }
+            for (int k = 0; k < P; ++k) CHECK(hipStreamWaitEvent(nullptr, ek[k], 0));
+        };
+        auto batch = [&](int L) {  // the same tiles per layer, P tokens
+            for (int l = 0; l < L; ++l) {
+                const E *in = l == 0 ? xb : ((l - 1) & 1 ? c1 : c0);
+                E *out = l == L - 1 ? yb : (l & 1 ? c1 : c0);
+                if (l % 2 == 0)
+                    hipLaunchKernelGGL((ring3_mfma_kernel<CU, false>), dim3(GU::NBLK, (P + GU::TT - 1) / GU::TT),
+                                       dim3(NT), 0, nullptr, in, layers[l].fk, layers[l].sk,
+                                       layers[l].lk, (void *)out, P, 0, (const void *)nullptr);
+                else
+                    hipLaunchKernelGGL((ring3_mfma_kernel<CD, false>), dim3(GD::NBLK, (P + GD::TT - 1) / GD::TT),
+                                       dim3(NT), 0, nullptr, in, layers[l].fk, layers[l].sk,
+                                       layers[l].lk, (void *)out, P, 0, (const void *)nullptr);
+            }
+        };
+        for (int L : Ls) {
+            const int reps = std::max(2, 500 / L);
+            for (int k = 0; k < P; ++k) {
+                CHECK(hipMemset(py[k], 0xff, MAXF * sizeof(E)));
+                CHECK(hipMemset(pxcc[k], 0xff, sizeof(unsigned) * NWG));
+            }
+            all(L);
+            per_layer(L, nullptr);
+            CHECK(hipDeviceSynchronize());
+            const int outn = L % 2 == 1 ? 2880 : 1920;
+            std::vector<E> h2(outn), h1(outn);
+            CHECK(hipMemcpy(h2.data(), yr, outn * sizeof(E), hipMemcpyDeviceToHost));
+            size_t diff = 0;
+            int timeouts = 0;
+            std::string ids;
+            for (int k = 0; k < P; ++k) {
+                CHECK(hipMemcpy(h1.data(), py[k], outn * sizeof(E), hipMemcpyDeviceToHost));
+                for (int i = 0; i < outn; ++i) diff += std::memcmp(&h1[i], &h2[i], sizeof(E)) != 0;
+                int herr = 0;
+                CHECK(hipMemcpy(&herr, perr[k], sizeof(int), hipMemcpyDeviceToHost));
+                timeouts += herr;
+                std::vector<unsigned> hids(NWG);
+                CHECK(hipMemcpy(hids.data(), pxcc[k], sizeof(unsigned) * NWG, hipMemcpyDeviceToHost));
+                std::sort(hids.begin(), hids.end());
+                hids.erase(std::unique(hids.begin(), hids.end()), hids.end());
+                ids += k ? ", [" : "[";
+                for (size_t j = 0; j < hids.size(); ++j)
+                    ids += (j ? ", " : "") + std::to_string(int(hids[j]));
+                ids += "]";
+            }
+            if (timeouts) {
+                std::printf("{\"form\": \"one_xcd_parallel\", \"stacks\": %d, \"layers\": %d, "
+                            "\"error\": \"a barrier reached its spin bound\", \"xcd_ids\": [%s]}\n",
+                            P, L, ids.c_str());
+                continue;
+            }
+            const float t_all = time_us([&] { all(L); }, reps);
+            const float t_one = time_us([&] { launch_k(0, L, nullptr); }, reps);
+            const float t_batch = time_us([&] { batch(L); }, reps);
+            std::printf("{\"form\": \"one_xcd_parallel\", \"stacks\": %d, \"rank\": %d, \"layers\": %d, "
+                        "\"parallel_us\": %.3f, \"one_stack_us\": %.3f, \"batched_per_layer_us\": %.3f, "
+                        "\"outputs_differing\": %zu, \"outputs\": %d, \"xcd_ids\": [%s]}\n",
+                        P, R, L, t_all, t_one, t_batch, diff, outn * P, ids.c_str());
+        }
+        return 0;
+    }
+#endif
     const bool prefetch_modes[2] = {false, true};
     for (int L : Ls) {
         const int reps = std::max(2, 2000 / L);

@@ -2,12 +2,16 @@
 
     python kernel-task_amd/benchmarks/stack_bench.py --build            (any machine with hipcc)
     python kernel-task_amd/benchmarks/stack_bench.py --out stack.json [--tokens 1] [--layers 8,32,128]
+    python kernel-task_amd/benchmarks/stack_bench.py --parallel 8 --out par.json   (P stacks side by side)
 
 Builds kernel-task_amd/benchmarks/_bin/stack_bench_{all,xcd} against libtrk.so (the same
 compiler flags as the library) and, on an MI355X, runs both: every XCD with a device-scope
 barrier, and one XCD with an L2 barrier (with and without prefetching the next layer's core
 slices across it). Each line compares the stack with the same tiles launched once per layer,
 eagerly and in a HIP graph, and checks that the stack's output equals theirs bit for bit.
+--parallel P runs P one-XCD stacks at once, stack k on XCD k (P sequences through the same
+layers), against one stack alone and the same tiles launched per layer for a batch of P
+tokens.
 
 Role of the reference's stack experiment and its one-GPU measurement plan
 (kernel_work/stack/tr_stack.cu:1-40, kernel-design/WEIGHT_STATIONARY.md:104-147).
@@ -52,13 +56,18 @@ def build(verbose: bool = False) -> list[Path]:
     return out
 
 
-def run(form: str, tokens: int, layers: list[int], timeout: float = 240.0) -> list[dict]:
-    """Run one form; returns its JSON lines. Raises if the program fails or reports an error."""
+def run(form: str, tokens: int, layers: list[int], timeout: float = 240.0,
+        parallel: int = 0) -> list[dict]:
+    """Run one form (with `parallel` > 0: that many one-XCD stacks side by side); returns its
+    JSON lines. Raises if the program fails or reports an error."""
+    import os
+
     path = binary(form)
     if not path.exists():
         raise RuntimeError(f"{path} is not built; run with --build first")
+    env = dict(os.environ, STACK_PAR=str(parallel)) if parallel else None
     done = subprocess.run([str(path), str(tokens), *map(str, layers)], capture_output=True,
-                          text=True, timeout=timeout)
+                          text=True, timeout=timeout, env=env)
     rows = [json.loads(ln) for ln in done.stdout.splitlines() if ln.startswith("{")]
     if done.returncode != 0 or any("error" in r for r in rows):
         raise RuntimeError(f"{path.name} failed ({done.returncode}):\n{done.stdout}\n{done.stderr}")
@@ -71,6 +80,8 @@ def main() -> int:
     ap.add_argument("--out", type=Path)
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--layers", default="8,32,128")
+    ap.add_argument("--parallel", type=int, default=0, metavar="P",
+                    help="run P one-XCD stacks side by side (1-8) instead of the two forms")
     args = ap.parse_args()
     if args.build:
         for p in build(verbose=True):
@@ -78,6 +89,19 @@ def main() -> int:
         return 0
     layers = [int(v) for v in args.layers.split(",")]
     rows = []
+    if args.parallel:
+        for r in run("xcd", 1, layers, parallel=args.parallel):
+            rows.append(r)
+            L, P = r["layers"], r["stacks"]
+            print(f"{P} one-XCD stacks L={L:4d}: {r['parallel_us'] / L:.3f} us per layer for all "
+                  f"{P} ({r['parallel_us'] / L / P:.3f} per sequence-layer), one stack "
+                  f"{r['one_stack_us'] / L:.3f}, per-layer launches of {P} tokens "
+                  f"{r['batched_per_layer_us'] / L:.3f}; outputs differing "
+                  f"{r['outputs_differing']} of {r['outputs']}; XCDs {r['xcd_ids']}", flush=True)
+        if args.out:
+            args.out.parent.mkdir(parents=True, exist_ok=True)
+            args.out.write_text(json.dumps({"rows": rows}, indent=1) + "\n")
+        return 0
     for form in FORMS:
         for r in run(form, args.tokens, layers):
             rows.append(r)
