@@ -37,3 +37,25 @@ def test_stack_matches_per_layer_launches(form, tokens):
         assert r["outputs_differing"] == 0, r
         assert r["barrier_timeouts"] == 0, r
         assert r["outputs"] == (2880 if r["layers"] % 2 else 1920) * tokens
+
+
+def test_stacks_side_by_side_each_on_its_own_xcd():
+    """Two one-XCD stacks at once on two streams: each keeps the workgroups on its own XCD
+    (XCC_ID), both outputs equal the per-layer launches."""
+    print("case: 2 one-XCD stacks side by side, layers=2,7", flush=True)
+    try:
+        rows = stack_bench.run("xcd", 1, [2, 7], timeout=120, parallel=2)
+    except RuntimeError as e:
+        # a stack whose workgroups were not dealt one residue class per XCD ends its
+        # barriers at the spin bound and reports it: the form does not apply there
+        if "spin bound" in str(e):
+            pytest.skip("the dispatcher did not deal the workgroups round-robin")
+        raise
+    assert len(rows) == 2
+    if any(r["units_missing"] for r in rows):
+        pytest.skip(f"the dispatcher did not deal the workgroups round-robin: {rows}")
+    for r in rows:
+        print(r, flush=True)
+        ids = r["xcd_ids"]
+        assert len(ids) == 2 and all(len(x) == 1 for x in ids) and ids[0] != ids[1], r
+        assert r["outputs_differing"] == 0 and r["outputs"] == 2 * (2880 if r["layers"] % 2 else 1920), r
