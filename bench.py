@@ -10,13 +10,17 @@ N(0,1) x (generator seed 0 + T), as the reference harness draws them
 its HIP-event stream latency in us/call over exactly K back-to-back calls, bracketed by
 synchronizes, with x and the packed cores resident in HBM.
 
-The same line carries the other metric cases (tokens 8/32 at rank 8, 1/32 at rank 16, and
-the bf16 Llama-shaped configs) with the dense GEMM of the same shape (F.linear on the
-materialised weight, timed the same way), the dominant kernel's roofline, the launch floors
-and the CPU baseline (the oracle's port of the reference path and the package's torch
-restatement of it, fp32, timed on this host). Every case is checked against the fp32
-factorized path after timing; a result outside the acceptance tolerance ends the run with a
-non-zero status and no JSON line.
+The line (the last line on stdout, kept under LINE_LIMIT bytes) carries the headline, the
+dominant kernel's roofline, the CPU baseline (the package's torch restatement of the
+reference path and the oracle's port of it, fp32, timed on this host) and one compact row per
+metric case (tokens 8/32 at rank 8, 1/32 at rank 16, the bf16 Llama-shaped configs and
+config 1 in fp32): stream time, the dense GEMM of the same shape (F.linear on the materialised
+weight, timed the same way) and roofline fractions. Kernel-only durations are not measured in
+process (every in-process source reads short kernels long); the roofline quotes the committed
+rocprofv3 kernel trace of the headline kernel beside its stream figure. The full per-case
+records, floors and memory figures go to DETAILS (and a summary line per case to stderr).
+Every case is checked against the fp32 factorized path after timing; a result outside the
+acceptance tolerance ends the run with a non-zero status and no JSON line.
 """
 from __future__ import annotations
 
@@ -43,6 +47,9 @@ sys.path.insert(0, str(ROOT / "kernel-task_amd"))
 sys.path.insert(0, str(ROOT))
 
 METRIC = "µs/call HIP-event latency, tokens 1/8/32, rank 8/16, vs dense fp16 GEMM"
+# the run record keeps about the last 10 KB of stdout: the one line stays well inside it
+LINE_LIMIT = 8000
+DETAILS = ROOT / "gpurun_out" / "bench_details.json"
 H100_PUBLISHED_R8_T1_US = 8.18  # ours-B stream, R8 t1, H100 SXM5
 
 CASES = [  # (label, input modes, output modes, rank, dtype, init, tokens)
@@ -66,8 +73,7 @@ def log(msg: str) -> None:
 TOLERANCE = {"float16": 2e-2, "bfloat16": 2e-2, "float32": 1e-4}
 
 
-def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup, headline,
-                 profile_kernels=True):
+def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup, headline):
     import torch
 
     from factorized_inference import (TRSpec, dense_forward, make_cores,
@@ -120,29 +126,24 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
         host_dense = statistics.median(m.host_us(dense, 50))
         submit_us = m.host_submit_us(ours, min(200, calls))
         # device memory of one call beyond its output (y stays allocated): nothing, no
-        # workspace and no counters
+        # workspace and no counters. Only this case's inputs are alive when the peak is
+        # reset (the previous token count's outputs were released at the end of its turn)
         m.synchronize()
         torch.cuda.reset_peak_memory_stats()
         y = run(x)
         m.synchronize()
         call_extra = torch.cuda.max_memory_allocated() - torch.cuda.memory_allocated()
-        # kernel-only device time per dispatch (torch.profiler over 20 back-to-back calls,
-        # the reference's tools/measure_kernels.py:69-82 protocol)
-        kernel = None
-        if profile_kernels:
-            times = m.kernel_us(ours, 20)
-            ring = {k: v for k, v in times.items() if "ring3" in k}
-            if ring:
-                name, kernel = max(ring.items(), key=lambda kv: kv[1]["dispatches"])
         # correctness after timing, against the fp32 factorized path on the same cores
-        y = y.float()
+        yf = y.float()
         ref = tr_forward_reference(x.float(), [c.float() for c in cores], spec)
-        diff = (y - ref).abs()
+        diff = (yf - ref).abs()
         err = diff.max().item()
         tol = TOLERANCE[dtype_name]
-        ok = bool((diff <= tol + tol * ref.abs()).all().item()) and bool(torch.isfinite(y).all())
+        ok = bool((diff <= tol + tol * ref.abs()).all().item()) and bool(torch.isfinite(yf).all())
         if dtype_name != "float32":
             ok = ok and err <= 1e-2 * ref.abs().max().item()
+        max_ref = ref.abs().max().item()
+        del y, yf, ref, diff
         info = run.selected(T)
         ref_flops = m.reference_flops(spec, T)
         peak = m.PEAK_TFLOPS[dtype]
@@ -154,7 +155,7 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
             "speedup_vs_dense": dense_us / ours_us,
             "ours_host_us": host_ours, "dense_host_us": host_dense, "ours_submit_us": submit_us,
             "flops": info["flops"], "bytes": info["bytes"],
-            "max_abs_err_vs_fp32": err, "max_abs_ref": ref.abs().max().item(),
+            "max_abs_err_vs_fp32": err, "max_abs_ref": max_ref,
             "prepare_ms": prep_ms, "packed_bytes": run.packed_bytes,
             "prepare_held_bytes": prep_held, "prepare_peak_bytes": prep_peak,
             "call_extra_bytes": call_extra,
@@ -166,16 +167,7 @@ def measure_case(label, ins, outs, rank, dtype_name, init, tokens, steps, warmup
             "reference_flops": ref_flops,
             "frac_mfma_reference_flops": ref_flops / (ours_us * 1e-6) / 1e12 / peak,
         }
-        if kernel is not None:
-            case.update({
-                "kernel_us": kernel["avg_us"], "kernel_min_us": kernel["min_us"],
-                "kernel_frac_hbm": info["bytes"] / (kernel["avg_us"] * 1e-6) / 1e9 / m.PEAK_HBM_GBS,
-                "kernel_frac_mfma": info["flops"] / (kernel["avg_us"] * 1e-6) / 1e12 / peak,
-                "kernel_frac_mfma_reference_flops":
-                    ref_flops / (kernel["avg_us"] * 1e-6) / 1e12 / peak,
-            })
         log(f"{label} T={T}: ours {ours_us:.2f} us, dense {dense_us:.2f} us, "
-            f"kernel {kernel['avg_us'] if kernel else float('nan'):.2f} us, "
             f"err {err:.2e}{'' if ok else ' FAILED'}, {info['name']}")
         results.append(case)
     return results
@@ -363,7 +355,7 @@ def runtime_default_child(steps: int, warmup: int) -> int:
         del a
         label, ins, outs, rank, dt, init, _ = CASES[0]
         case = measure_case(label, ins, outs, rank, dt, init, (1,), steps, warmup,
-                            headline=True, profile_kernels=False)[0]
+                            headline=True)[0]
         from factorized_inference import TRSpec, make_cores, prepare_optimized
 
         spec = TRSpec(ins, outs, rank)
@@ -404,9 +396,6 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true")
-    ap.add_argument("--no-kernel-profiler", action="store_true",
-                    help="skip the in-process torch.profiler kernel times (for runs under "
-                         "rocprofv3, which traces the same dispatches itself)")
     ap.add_argument("--no-runtime-default", action="store_true",
                     help="skip the child process that times the headline under the runtime's "
                          "default kernel-argument placement")
@@ -439,7 +428,6 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
     torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
     torch.set_num_threads(1)
-    profile = not args.no_kernel_profiler
     with torch.inference_mode():
         # bring the GPU to its working clock before the first case (dense GEMMs, untimed)
         a = torch.randn(4096, 4096, device="cuda", dtype=torch.float16)
@@ -454,8 +442,8 @@ def main() -> int:
             if args.headline_only and i > 0:
                 break
             cases += measure_case(label, ins, outs, rank, dt, init, tokens, args.steps,
-                                  args.warmup, headline=(i == 0), profile_kernels=profile)
-        floors = m.floors(_lib.load(), profiler=profile)
+                                  args.warmup, headline=(i == 0))
+        floors = m.floors(_lib.load())
         xcd_local = None if args.headline_only else xcd_local_figure(args.steps, args.warmup)
     failed = [f"{c['case']} T={c['tokens']}" for c in cases if not c["passed"]]
     if xcd_local is not None and not xcd_local["passed"]:
@@ -463,33 +451,100 @@ def main() -> int:
     if failed:
         log(f"results outside the acceptance tolerance: {', '.join(failed)}; no bench line")
         return 1
-    head = cases[0]
     default_runtime = None if args.no_runtime_default else runtime_default_figure(
         args.steps, args.warmup)
     traffic = None
     traffic_file = ROOT / "profiles" / "traffic_r8_t1.json"
     if traffic_file.exists():
         traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    details = {"cases": cases, "floors": floors, "xcd_local": xcd_local, "cpu_baseline": cpu,
+               "runtime_default": default_runtime}
+    try:
+        DETAILS.parent.mkdir(parents=True, exist_ok=True)
+        DETAILS.write_text(json.dumps(details, indent=1) + "\n")
+        details_path = str(DETAILS.relative_to(ROOT))
+    except OSError as exc:
+        log(f"could not write {DETAILS}: {exc}")
+        details_path = None
+    emit(build_line(args.steps, args.warmup, cases, floors, xcd_local, cpu, default_runtime,
+                    traffic, details_path, m.PEAK_HBM_GBS))
+    return 0
+
+
+# per-case row of the line: (column, case key, digits)
+CASE_COLUMNS = [
+    ("case", "case", None), ("T", "tokens", None), ("ours_us", "ours_stream_us", 2),
+    ("dense_us", "dense_stream_us", 2), ("frac_hbm", "frac_hbm", 5),
+    ("frac_mfma", "frac_mfma", 4), ("frac_mfma_ref_flops", "frac_mfma_reference_flops", 4),
+    ("err", "max_abs_err_vs_fp32", 6),
+    ("extra_bytes", "call_extra_bytes", None), ("variant", "variant", None),
+]
+
+
+def _rounded(v, digits):
+    if v is None or digits is None or not isinstance(v, float):
+        return v
+    return float(f"{v:.{digits}g}") if abs(v) < 1 else round(v, digits)
+
+
+def trace_kernel_figure(variant: str) -> dict | None:
+    """The headline kernel's mean dispatch duration in the committed rocprofv3 kernel trace
+    (profiles/ring3_kernel_trace.json, written by benchmarks/counters.py grids from a traced
+    run of this script), if that trace is of the same variant."""
+    path = ROOT / "profiles" / "ring3_kernel_trace.json"
+    try:
+        rows = json.loads(path.read_text())["rows"]
+    except (OSError, KeyError, ValueError):
+        return None
+    for r in rows:
+        if r.get("variant") == variant and r.get("case") == "r8" and r.get("tokens") == 1:
+            return {"mean_us": r["trace_mean_us"], "source": f"rocprofv3 --kernel-trace, "
+                    f"{r['trace_dispatches']} dispatches (profiles/ring3_kernel_trace.json)"}
+    return None
+
+
+def build_line(steps, warmup, cases, floors, xcd_local, cpu, default_runtime, traffic,
+               details_path, peak_hbm_gbs) -> dict:
+    """The driver's JSON line: headline fields, the dominant kernel's roofline, the CPU
+    baseline and a compact row per case (columns CASE_COLUMNS). Long fields (variant names,
+    then the runtime-default and XCD-local figures) are dropped if the line would exceed
+    LINE_LIMIT bytes; the full records are in the details file."""
+    head = cases[0]
     achieved = head["achieved_GBps"]
-    roof = {"bound": "hbm", "achieved": achieved, "peak": m.PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": achieved / m.PEAK_HBM_GBS, "traffic": traffic,
+    roof = {"bound": "hbm", "achieved": achieved, "peak": peak_hbm_gbs, "unit": "GB/s",
+            "frac": achieved / peak_hbm_gbs, "traffic": traffic,
             "kernel": head["variant"], "algorithmic_bytes": head["bytes"],
-            "time_us": head["ours_stream_us"], "time_source": "HIP events over the timed block",
+            "time_us": head["ours_stream_us"],
+            "time_source": "HIP events over the timed block, divided by its launches",
             "mfma_frac": head["frac_mfma"],
             "mfma_frac_reference_flops": head["frac_mfma_reference_flops"],
-            "floor_stream_empty_args_us": floors["stream_empty_launch_args_us"],
-            "floor_stream_empty_us": floors["stream_empty_launch_us"]}
-    if "kernel_us" in head:
-        roof.update({"kernel_us": head["kernel_us"], "kernel_frac": head["kernel_frac_hbm"],
-                     "kernel_time_source": "torch.profiler kernel events, 20 back-to-back calls",
-                     "floor_kernel_empty_args_us": floors.get("kernel_empty_args_us")})
+            "floor_stream_empty_args_us": floors.get("stream_empty_launch_args_us"),
+            "floor_stream_empty_us": floors.get("stream_empty_launch_us")}
+    trace = trace_kernel_figure(head["variant"])
+    if trace is not None:
+        roof.update({"trace_kernel_us": trace["mean_us"],
+                     "trace_kernel_frac": head["bytes"] / (trace["mean_us"] * 1e-6) / 1e9 /
+                     peak_hbm_gbs, "trace_source": trace["source"]})
+    cpu_short = None
+    if cpu is not None:
+        cpu_short = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",
+                                         "oracle_port_us", "host_threads", "cpu_model")}
+        cpu_short["torch_path_us_by_threads"] = {
+            n: round(v["us"], 1) for n, v in cpu["torch_reference_path_us"].items()}
+    runtime = None
+    if default_runtime is not None:
+        runtime = {k: default_runtime.get(k) for k in ("value", "median_of_9_blocks", "submit_us")}
+    xcd = None
+    if xcd_local is not None:
+        xcd = {k: xcd_local.get(k) for k in ("variant", "value", "default_value", "traffic")}
     line = {
         "metric": METRIC,
         "value": head["ours_stream_us"],
         "unit": "us/call",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": head["ours_stream_us"] / 1000.0,
         "higher_is_better": False,
         "scaling": "weak",
@@ -501,16 +556,30 @@ def main() -> int:
                                "rank 8, fp16, tokens 1 (BASELINE configs[1])",
                    "tokens": 1, "rank": 8, "in_features": 1920, "out_features": 2880,
                    "hip_force_dev_kernarg": os.environ.get("HIP_FORCE_DEV_KERNARG"),
-                   "runtime_default": default_runtime},
+                   "runtime_default": runtime},
         "dense_stream_us": head["dense_stream_us"],
         "roofline": roof,
-        "xcd_local": xcd_local,
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
-        "floors": floors,
-        "cases": cases,
+        "cpu_baseline": cpu_short,
+        "xcd_local": xcd,
+        "case_columns": [c for c, _, _ in CASE_COLUMNS],
+        "cases": [[_rounded(c.get(k), d) for _, k, d in CASE_COLUMNS] for c in cases],
+        "details": details_path,
     }
+    if len(json.dumps(line)) > LINE_LIMIT:
+        line["case_columns"] = line["case_columns"][:-1]
+        line["cases"] = [row[:-1] for row in line["cases"]]
+    for key in ("xcd_local", "details"):
+        if len(json.dumps(line)) > LINE_LIMIT:
+            line.pop(key)
+    if len(json.dumps(line)) > LINE_LIMIT:
+        line["config"]["runtime_default"] = None
+    return line
+
+
+def emit(line: dict) -> None:
+    """Prints the line as the last thing on stdout (everything else goes to stderr)."""
+    sys.stdout.flush()
     print(json.dumps(line), flush=True)
-    return 0
 
 
 if __name__ == "__main__":

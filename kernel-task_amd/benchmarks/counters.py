@@ -8,8 +8,12 @@ kernel traces.
     # back-to-back blocks of one kernel in a --kernel-trace run (e.g. bench.py's timed block)
     python kernel-task_amd/benchmarks/counters.py blocks TRACE.csv --kernel REGEX [--grid N]
     # durations per (tensor-ring kernel, grid) in a --kernel-trace run: one kernel serves
-    # several token counts (grids), which rocprofv3's --stats summary lumps together
+    # several token counts (grids), which rocprofv3's --stats summary lumps together; each
+    # row also gives the longest back-to-back block of that kernel and grid
     python kernel-task_amd/benchmarks/counters.py grids TRACE.csv [--out FILE.json]
+    # one row per bench.py case: its kernel's durations in a traced bench.py run, beside the
+    # case's stream time from that run's details file (gpurun_out/bench_details.json)
+    python kernel-task_amd/benchmarks/counters.py cases TRACE.csv DETAILS.json [--out FILE]
 
 A probe run (bench.py --traffic-probe CALLS) launches one tensor-ring kernel CALLS times and
 then copies a 512 MiB buffer 5 times. The copy is larger than every L2 and the 256 MB MALL,
@@ -127,9 +131,26 @@ def blocks(trace: Path, pattern: str, grid: int | None = None, max_gap_us: float
     return out
 
 
-def grids(trace: Path) -> list[dict]:
+def _longest_block(spans: list[tuple[int, int]], max_gap_us: float) -> list[tuple[int, int]]:
+    """The longest run of consecutive (start, end) spans whose gaps from the previous end stay
+    under max_gap_us (spans sorted by start)."""
+    best, cur, prev_end = [], [], None
+    for s, e in spans:
+        if prev_end is not None and (s - prev_end) / 1e3 > max_gap_us:
+            cur = []
+        cur.append((s, e))
+        prev_end = e
+        if len(cur) > len(best):
+            best = list(cur)
+    return best
+
+
+def grids(trace: Path, max_gap_us: float = 30.0) -> list[dict]:
     """Per (tensor-ring or empty kernel, grid in workgroups x * y): dispatches and mean, min
-    and median duration in us, most dispatched first."""
+    and median duration in us over every dispatch, most dispatched first; and the longest
+    back-to-back block of that kernel and grid (dispatches whose gaps stay under max_gap_us:
+    bench.py's timed blocks and its per-dispatch kernel timing), with its mean duration and
+    its period (first start to last end over dispatches)."""
     acc: dict = defaultdict(list)
     with open(trace, newline="") as f:
         for r in csv.DictReader(f):
@@ -142,14 +163,65 @@ def grids(trace: Path) -> list[dict]:
             wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"])
             g = (int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]),
                  int(r["Grid_Size_Y"]) // int(r["Workgroup_Size_Y"]))
-            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-            acc[(label, g, wg)].append(d)
+            acc[(label, g, wg)].append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     out = []
-    for (label, g, wg), d in acc.items():
-        d.sort()
+    for (label, g, wg), spans in acc.items():
+        spans.sort()
+        d = sorted((e - s) / 1e3 for s, e in spans)
+        block = _longest_block(spans, max_gap_us)
+        bd = [(e - s) / 1e3 for s, e in block]
         out.append({"kernel": label, "grid": list(g), "threads": wg, "dispatches": len(d),
-                    "mean_us": sum(d) / len(d), "min_us": d[0], "median_us": d[len(d) // 2]})
+                    "mean_us": sum(d) / len(d), "min_us": d[0], "median_us": d[len(d) // 2],
+                    "block_dispatches": len(block), "block_mean_us": sum(bd) / len(bd),
+                    "block_period_us": (block[-1][1] - block[0][0]) / 1e3 / len(block)})
     return sorted(out, key=lambda r: -r["dispatches"])
+
+
+def kcfg_of(label: str) -> tuple[tuple, tuple] | None:
+    """(chain order, tile fields TT..XL) of a 'ring3<KCfg fields>' label; fields the
+    compiler's name leaves out at the end are zero."""
+    m = re.fullmatch(r"ring3<([-0-9,]*)>", label)
+    if not m:
+        return None
+    f = [int(v) for v in m.group(1).split(",") if v]
+    f += [0] * (24 - len(f))
+    return tuple(f[1:4]), tuple(f[11:24])
+
+
+def cases(trace: Path, details: dict, max_gap_us: float = 30.0) -> list[dict]:
+    """Per bench.py case (details["cases"], from the traced run): the kernel of its variant at
+    its grid in the trace, with dispatches, mean / min / median duration and the longest
+    back-to-back block (grids()), the case's stream time in the same run, and the roofline
+    fractions of the trace mean (algorithmic bytes / 8 TB/s, chain-order flops / peak)."""
+    import dataclasses
+
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    from factorized_inference import tilegen
+
+    peaks = {"float16": 2500.0, "bfloat16": 2500.0, "float32": 157.3}
+    by_cfg: dict = {}
+    for r in grids(trace, max_gap_us):
+        key = kcfg_of(r["kernel"])
+        if key is not None:
+            by_cfg[(key, tuple(r["grid"]))] = r
+    out = []
+    for c in details["cases"]:
+        order, tile = tilegen.parse_variant_name(c["variant"])
+        key = ((tuple(order), dataclasses.astuple(tile)), tuple(c["grid"][:2]))
+        r = by_cfg.get(key)
+        row = {"case": c["case"], "tokens": c["tokens"], "variant": c["variant"],
+               "grid": c["grid"][:2], "stream_us": c["ours_stream_us"]}
+        if r is not None:
+            mean = r["mean_us"]
+            row.update({"trace_dispatches": r["dispatches"], "trace_mean_us": mean,
+                        "trace_min_us": r["min_us"], "trace_median_us": r["median_us"],
+                        "trace_block_dispatches": r["block_dispatches"],
+                        "trace_block_mean_us": r["block_mean_us"],
+                        "trace_block_period_us": r["block_period_us"],
+                        "trace_frac_hbm": c["bytes"] / (mean * 1e-6) / 1e9 / 8000.0,
+                        "trace_frac_mfma": c["flops"] / (mean * 1e-6) / 1e12 / peaks[c["dtype"]]})
+        out.append(row)
+    return out
 
 
 def main() -> int:
@@ -171,7 +243,18 @@ def main() -> int:
     gp = sub.add_parser("grids")
     gp.add_argument("trace", type=Path)
     gp.add_argument("--out", type=Path)
+    cp = sub.add_parser("cases")
+    cp.add_argument("trace", type=Path)
+    cp.add_argument("details", type=Path)
+    cp.add_argument("--out", type=Path)
     args = ap.parse_args()
+    if args.cmd == "cases":
+        res = {"trace": str(args.trace), "rows": cases(args.trace, json.loads(args.details.read_text()))}
+        text = json.dumps(res, indent=1) + "\n"
+        if args.out:
+            args.out.write_text(text)
+        print(text, end="")
+        return 0
     if args.cmd == "grids":
         text = json.dumps(grids(args.trace), indent=1) + "\n"
         if args.out:

@@ -96,8 +96,10 @@ def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Pa
         resources.update(json.loads(obj.with_suffix(".resources.json").read_text()))
     RESOURCES.write_text(json.dumps(resources, indent=0, sort_keys=True) + "\n")
     tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objects), "-ldl"]
+    # the SONAME lets the variant modules' dependency on libtrk.so resolve to the copy this
+    # process already loaded, wherever the tree lives (they carry no path to it)
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libtrk.so",
+           "-o", str(tmp), *map(str, objects), "-ldl"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

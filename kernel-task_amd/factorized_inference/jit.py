@@ -1,7 +1,7 @@
 """Variant modules built at prepare time for shapes the library has no MFMA tables for.
 
 libtrk.so carries MFMA kernels for the declared shapes only (tilegen.DECLARED); a plan for
-any other shape would run the generic VALU kernel. For fp16 and bf16 plans,
+any other shape would run the generic VALU kernel. For fp16, bf16 and fp32 plans,
 PreparedTRKernel asks this module for a variant module instead:
 
   1. the kernel rank: the cores' rank if it is a power of two >= 8, else the next such power
@@ -13,7 +13,9 @@ PreparedTRKernel asks this module for a variant module instead:
      or $TRK_JIT_DIR), named by a hash of the table, the kernel headers and the compiler
      flags, so a changed header or table builds a new module and an unchanged one is reused
      across processes;
-  4. trk_plan_load_module checks the module's ABI and plan layout and adds its variants.
+  4. trk_plan_load_module checks the module's ABI and plan layout and adds its variants. The
+     module names libtrk.so as a dependency without a path; the copy the process has loaded
+     (SONAME libtrk.so) satisfies it, so a tree copied elsewhere works unchanged.
 
 This is the role of the reference's first-use build of its extension (tr_kernel.py:31-57,
 torch.utils.cpp_extension.load: about a minute the first time, then cached). A module build
@@ -34,6 +36,8 @@ PACKAGE = Path(__file__).resolve().parent
 CACHE = Path(os.environ.get("TRK_JIT_DIR", PACKAGE.parent / "_jit"))
 HEADERS = ("trk_mfma_kernel.h", "trk_internal.h", "trk_types.h")
 MAX_KERNEL_RANK = 32
+# how a module links (hashed with the source): libtrk.so by name only, no run path
+LINK_FLAGS = ("-shared", "-fvisibility=hidden", "-l:libtrk.so")
 
 
 def enabled() -> bool:
@@ -69,6 +73,7 @@ def _fingerprint(src: str) -> str:
     # and the headers they point to are hashed above, so a copy of the tree elsewhere (a
     # GPU box) reuses the modules built here
     h.update(" ".join(f for f in build_ext.HIPCC_FLAGS if not f.startswith("-I")).encode())
+    h.update(" ".join(LINK_FLAGS).encode())
     return h.hexdigest()[:16]
 
 
@@ -97,9 +102,11 @@ def build_module(shape: tilegen.ShapeDecl, verbose: bool = False) -> Path | None
         source = path.with_suffix(".hip")
         source.write_text(src)
         tmp = path.with_name(path.name + f".tmp{os.getpid()}")
-        cmd = [build_ext._hipcc(), *build_ext.HIPCC_FLAGS, "-shared", "-fvisibility=hidden",
-               "-x", "hip", str(source), "-o", str(tmp), f"-L{PACKAGE}", "-l:libtrk.so",
-               f"-Wl,-rpath,{PACKAGE}"]
+        # no run path: the module is only ever loaded into a process that has loaded
+        # libtrk.so (trk_plan_load_module), whose SONAME satisfies the dependency, so a copy
+        # of the tree at another path binds to its own library and never to this checkout's
+        cmd = [build_ext._hipcc(), *build_ext.HIPCC_FLAGS, "-x", "hip", str(source), "-o",
+               str(tmp), f"-L{PACKAGE}", *LINK_FLAGS]
         if verbose:
             print(" ".join(cmd), flush=True)
         done = subprocess.run(cmd, capture_output=True, text=True)

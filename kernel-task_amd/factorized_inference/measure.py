@@ -5,12 +5,13 @@ tools/measure_kernels.py:36-103:
   stream latency   HIP events bracketing a block of back-to-back calls on the current
                    stream, divided by the block length (not a sum of kernel durations)
   host latency     wall clock around one call including the trailing synchronize
-  kernel time      device time per dispatch from torch.profiler kernel events over a block
-                   of back-to-back calls (tools/measure_kernels.py:69-82); on ROCm its
-                   timestamps bracket the dispatch as the tracer sees it, so a short kernel
-                   reads longer than its share of the stream period
+  kernel time      not measured in process. The reference reads profiler kernel events
+                   (tools/measure_kernels.py:69-82); on ROCm torch.profiler adds ~2.5-3.5 us
+                   and HIP events bound to the dispatch (hipExtLaunchKernel) ~1 us to kernels
+                   of a few microseconds, so both read above the stream period there. Kernel
+                   durations come from rocprofv3 kernel traces instead
   floors           an empty C call, and one empty kernel launch without and with the forward
-                   kernels' arguments (host and stream time, and profiler kernel time)
+                   kernels' arguments (host and stream time)
   work             algorithmic flops of the chain order the kernel runs, the reference's
                    flop count (its fixed order, tools/measure_kernels.py:36-44), and
                    compulsory bytes = element size x (factor parameters + T*in + T*out)
@@ -73,27 +74,6 @@ def host_submit_us(fn: Callable[[], object], calls: int) -> float:
     return (t1 - t0) / 1000.0 / calls
 
 
-def kernel_us(fn: Callable[[], object], calls: int = 20) -> dict[str, dict]:
-    """Per kernel name: dispatches and average / minimum device time per dispatch (us) from
-    torch.profiler's kernel events over `calls` back-to-back calls after 3 warm-up calls."""
-    from torch.autograd import DeviceType
-    from torch.profiler import ProfilerActivity, profile
-
-    for _ in range(3):
-        fn()
-    synchronize()
-    with profile(activities=[ProfilerActivity.CUDA]) as prof:
-        for _ in range(calls):
-            fn()
-        synchronize()
-    per: dict[str, list[float]] = {}
-    for ev in prof.events():
-        if ev.device_type == DeviceType.CUDA:
-            per.setdefault(ev.name, []).append(ev.time_range.elapsed_us())
-    return {name: {"dispatches": len(v), "avg_us": sum(v) / len(v), "min_us": min(v)}
-            for name, v in per.items()}
-
-
 def reference_flops(spec, tokens: int) -> float:
     """Flops of the reference's fixed contraction order (G1, G2, G3) for `tokens` tokens
     (tools/measure_kernels.py:36-44): the count its "% FP16 TC peak" column uses."""
@@ -104,10 +84,10 @@ def reference_flops(spec, tokens: int) -> float:
     return 2.0 * tokens * per_token
 
 
-def floors(lib, calls: int = 2000, profiler: bool = True) -> dict:
-    """Host cost of an empty C call and of an empty launch; stream time of empty launches;
-    with `profiler`, the profiler's kernel time of the empty kernels (the reference's
-    kernel_empty_us, tools/measure_kernels.py:97-103)."""
+def floors(lib, calls: int = 2000) -> dict:
+    """Host cost of an empty C call and of an empty launch; stream time of empty launches
+    (the reference's floors, tools/measure_kernels.py:97-103, without its profiler kernel
+    time of the empty kernel)."""
     from .tr_kernel import current_stream_handle
 
     dev = torch.cuda.current_device()
@@ -131,11 +111,6 @@ def floors(lib, calls: int = 2000, profiler: bool = True) -> dict:
         "stream_empty_launch_args_us": statistics.median(stream_us(launch_args, 200, blocks=5)),
         "stream_handle": bool(stream is not None),
     }
-    if profiler:
-        for key, fn in (("kernel_empty_us", launch), ("kernel_empty_args_us", launch_args)):
-            times = kernel_us(fn)
-            out[key] = sum(t["avg_us"] * t["dispatches"] for t in times.values()) / max(
-                1, sum(t["dispatches"] for t in times.values()))
     return out
 
 

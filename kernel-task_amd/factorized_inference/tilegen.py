@@ -643,6 +643,19 @@ def search_candidates(shape: ShapeDecl, extended: bool = False) -> dict[str, tup
     return out
 
 
+def add_candidate(cands: dict, name: str, order: tuple, tile: Tile) -> str | None:
+    """Adds (order, tile) to `cands` under `name`, or under `name#2`, `name#3`, ... when
+    another tile holds that name (shortened names of two refined winners can agree); a tile
+    already present is not added again. Returns the name used, or None."""
+    if (order, tile) in cands.values():
+        return None
+    unique, k = name, 2
+    while unique in cands:
+        unique, k = f"{name}#{k}", k + 1
+    cands[unique] = (order, tile)
+    return unique
+
+
 def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = False,
           extended: bool = False) -> list[tuple[str, tuple, Tile, int, int]]:
     """[(name, order, tile, t_min, t_max)] for one shape: the tuned winners when the shape
@@ -688,8 +701,7 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
                     found += [(base[:40] + suffix + tag, v)
                               for suffix, v in neighbours(shape, order, tile).items()]
             for n, t in found:
-                if (order, t) not in cands.values():
-                    cands[n] = (order, t)
+                add_candidate(cands, n, order, t)
     return [(n, o, t, *ranges.get(n, (0, 0))) for n, (o, t) in cands.items()]
 
 

@@ -86,13 +86,13 @@ def make_plan(spec: TRSpec, dtype: torch.dtype) -> _lib.Plan:
                                   krank, _TILEGEN_DTYPES[dtype])
         try:
             path = jit.build_module(shape)
+            if path is None:
+                return plan
+            padded.load_module(path)
         except (OSError, RuntimeError) as exc:
             warnings.warn(f"no MFMA variant module for {shape.key} ({exc}); the generic "
                           "kernel serves this shape", RuntimeWarning)
             return plan
-        if path is None:
-            return plan
-        padded.load_module(path)
     return padded if padded.has_mfma else plan
 
 

@@ -98,3 +98,45 @@ def test_blocks_split_at_gaps(tmp_path):
     assert [r["dispatches"] for r in b] == [12, 12]
     assert b[0]["mean_us"] == pytest.approx(3.0) and b[1]["start_us"] > b[0]["start_us"]
     assert counters.blocks(tmp_path / "t.csv", r"KCfg", grid=61440) == []
+
+
+def test_grids_report_the_longest_back_to_back_block(tmp_path):
+    # 3 isolated long dispatches (the tracer's spaced-out calls), then 20 back to back with
+    # 2.5 us duration and 3.0 us period: the block figures come from the 20 only
+    rows, t = [], 0
+    for _ in range(3):
+        rows.append((RING, 30720, 1, 256, t, t + 4000))
+        t += 100000
+    for _ in range(20):
+        rows.append((RING, 30720, 1, 256, t, t + 2500))
+        t += 3000
+    write_trace(tmp_path / "t.csv", rows)
+    (r,) = counters.grids(tmp_path / "t.csv")
+    assert r["dispatches"] == 23 and r["block_dispatches"] == 20
+    assert r["block_mean_us"] == pytest.approx(2.5)
+    assert r["block_period_us"] == pytest.approx((19 * 3000 + 2500) / 1e3 / 20)
+    assert r["mean_us"] == pytest.approx((3 * 4.0 + 20 * 2.5) / 23)
+
+
+def test_cases_match_each_bench_case_to_its_kernel_and_grid(tmp_path):
+    # the headline case's variant at grid 240 x 1; the same kernel at another grid and an
+    # unrelated kernel stay out of its row; a case with no traced kernel keeps its stream time
+    rows = [(RING, 240 * 256, 1, 256, 0, 3000), (RING, 240 * 256, 1, 256, 20000, 22000),
+            (RING, 240 * 256, 8, 256, 40000, 50000),
+            (RING.replace("8, 4, 1, 0, 16, 4}", "8, 4, 1, 0, 16, 8}"), 240 * 512, 1, 512,
+             60000, 70000)]
+    write_trace(tmp_path / "t.csv", rows)
+    details = {"cases": [
+        {"case": "r8", "tokens": 1, "variant": "ring3_mfma<210,1,1,2,12,8,4,1>",
+         "grid": [240, 1, 1], "ours_stream_us": 3.1, "bytes": 98688.0, "flops": 32.4e6,
+         "dtype": "float16"},
+        {"case": "r8", "tokens": 32, "variant": "ring3_mfma_wide4x32<210,1,2,10,12,4,2,1>",
+         "grid": [120, 32, 1], "ours_stream_us": 5.0, "bytes": 2e5, "flops": 1e9,
+         "dtype": "float16"}]}
+    head, other = counters.cases(tmp_path / "t.csv", details)
+    assert head["trace_dispatches"] == 2 and head["trace_mean_us"] == pytest.approx(2.5)
+    assert head["trace_frac_hbm"] == pytest.approx(98688 / 2.5e-6 / 1e9 / 8000)
+    assert head["stream_us"] == 3.1
+    assert "trace_mean_us" not in other and other["stream_us"] == 5.0
+    assert counters.kcfg_of(counters.kernel_label(RING)) == (
+        (2, 1, 0), (1, 1, 2, 12, 8, 4, 1, 0, 16, 4, 0, 0, 0))

@@ -86,3 +86,37 @@ def test_loader_rejects_other_libraries():
         plan.load_module(_trkcall.__file__)
     with pytest.raises(_lib.TrkError):
         plan.load_module("/nonexistent/trk_mod.so")
+
+
+def test_module_binds_to_the_library_of_a_relocated_tree(tmp_path):
+    # A copy of the tree at another path (a GPU box) loads its modules against its own
+    # libtrk.so: the module carries no path to the library, and the SONAME of the copy the
+    # process loaded satisfies its dependency. Checked in a fresh process that loads only
+    # the copy, with the maps listing exactly one libtrk.so.
+    import shutil
+    import subprocess
+    import sys
+
+    from factorized_inference import build_ext
+
+    shape = tilegen.ShapeDecl("prepared", (4, 6, 8), (6, 4, 8), 8, "f16")
+    built = jit.build_module(shape)
+    pkg = tmp_path / "moved" / "factorized_inference"
+    shutil.copytree(build_ext.PACKAGE, pkg, ignore=shutil.ignore_patterns("__pycache__"))
+    module = tmp_path / "moved" / "_jit" / built.name
+    module.parent.mkdir()
+    shutil.copy(built, module)
+    script = (
+        "import sys\n"
+        f"sys.path.insert(0, {str(pkg.parent)!r})\n"
+        "from factorized_inference import _lib\n"
+        "plan = _lib.Plan((4, 6, 8), (6, 4, 8), 8, _lib.DTYPE_F16)\n"
+        f"added = plan.load_module({str(module)!r})\n"
+        "maps = sorted({l.split()[-1] for l in open('/proc/self/maps') if 'libtrk.so' in l})\n"
+        "print(added, plan.has_mfma, *maps)\n")
+    done = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True,
+                          timeout=300)
+    assert done.returncode == 0, done.stderr[-2000:]
+    added, has_mfma, *maps = done.stdout.split()
+    assert int(added) > 0 and has_mfma == "True"
+    assert maps == [str(pkg / "libtrk.so")]

@@ -184,3 +184,17 @@ def test_rule_ranges_cover_everything():
         for lo, hi in ranges.values():
             covered[lo:min(hi, 299) + 1] = True
         assert covered[1:].all(), names
+
+
+
+def test_candidates_with_one_name_keep_both_tiles():
+    # shortened names of two refined winners can agree: the second tile gets a numbered
+    # name instead of replacing the first; an identical tile is not added twice
+    order = (2, 1, 0)
+    t1, t2 = tilegen.Tile(1, 1, 10, 12, 4, 2, 1), tilegen.Tile(1, 1, 10, 12, 2, 2, 1)
+    cands = {}
+    assert tilegen.add_candidate(cands, "w~t1", order, t1) == "w~t1"
+    assert tilegen.add_candidate(cands, "w~t1", order, t2) == "w~t1#2"
+    assert tilegen.add_candidate(cands, "w~t1", order, t1) is None
+    assert tilegen.add_candidate(cands, "w~t1", (0, 1, 2), t1) == "w~t1#3"
+    assert cands == {"w~t1": (order, t1), "w~t1#2": (order, t2), "w~t1#3": ((0, 1, 2), t1)}
