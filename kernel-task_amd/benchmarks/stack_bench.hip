@@ -15,8 +15,13 @@
 //                atomic in that L2 plus an L1 invalidation; split into arrive (after a layer)
 //                and wait (inside the next layer's first unit, once its core-slice loads are
 //                in flight, which do not depend on the activations)
-// Every barrier wait is bounded (it sets an error flag and gives up), and the launch is
-// cooperative, so the runtime refuses a grid whose workgroups could not all be resident.
+// Every barrier wait is bounded (it sets an error flag and gives up). The single stacks are
+// cooperative launches, so the runtime refuses a grid whose workgroups could not all be
+// resident; the side-by-side stacks (STACK_PAR) are plain launches, whose error flags are read
+// after every run, the timed ones included, and refuse the figure when a barrier gave up.
+// With STACK_DUMP=<dir> the program writes x, every layer's cores ([R][o][i][R], fp16) and
+// every checked output (the stacks' and the per-layer launches') as raw fp16 files there, for
+// a check against an independent restatement of each layer.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -234,17 +239,30 @@ int main(int argc, char **argv) {
         std::fprintf(stderr, "no packed chain for the stack's tiles\n");
         return 1;
     }
+    const char *dump = std::getenv("STACK_DUMP");
+    auto write_file = [&](const std::string &name, const void *data, size_t bytes) {
+        if (!dump) return;
+        const std::string path = std::string(dump) + "/" + name;
+        FILE *f = std::fopen(path.c_str(), "wb");
+        if (!f || std::fwrite(data, 1, bytes, f) != bytes) {
+            std::fprintf(stderr, "cannot write %s\n", path.c_str());
+            std::exit(1);
+        }
+        std::fclose(f);
+    };
     std::mt19937 rng(7);
     std::normal_distribution<float> nd(0.f, 1.f);
     // distinct cores per layer, per-core sigma (make_cores) so activations stay O(1)
     std::vector<void *> owned;
-    auto make_layer = [&](trk_plan *p, const int *in, const int *out, int chain) {
+    auto make_layer = [&](trk_plan *p, const int *in, const int *out, int chain, int l) {
         const double sig = std::pow(double(in[0] * in[1] * in[2]) * R * R * R, -1.0 / 6.0);
         void *g[3];
         for (int k = 0; k < 3; ++k) {
             const size_t n = size_t(R) * out[k] * in[k] * R;
             std::vector<E> h(n);
             for (auto &v : h) v = E(float(nd(rng) * sig));
+            write_file("core_l" + std::to_string(l) + "_k" + std::to_string(k) + ".bin", h.data(),
+                       n * sizeof(E));
             CHECK(hipMalloc(&g[k], n * sizeof(E)));
             CHECK(hipMemcpy(g[k], h.data(), n * sizeof(E), hipMemcpyHostToDevice));
         }
@@ -261,13 +279,15 @@ int main(int argc, char **argv) {
     };
     std::vector<Layer> layers;
     for (int l = 0; l < Lmax; ++l)
-        layers.push_back(l % 2 == 0 ? make_layer(pu, m_up, m_down, cu) : make_layer(pd, m_down, m_up, cd));
+        layers.push_back(l % 2 == 0 ? make_layer(pu, m_up, m_down, cu, l)
+                                    : make_layer(pd, m_down, m_up, cd, l));
     Layer *dlayers;
     CHECK(hipMalloc(&dlayers, sizeof(Layer) * Lmax));
     CHECK(hipMemcpy(dlayers, layers.data(), sizeof(Layer) * Lmax, hipMemcpyHostToDevice));
     constexpr int MAXF = 2880;  // widest activation row
     std::vector<E> hx(size_t(T) * 1920);
     for (auto &v : hx) v = E(nd(rng));
+    write_file("x.bin", hx.data(), hx.size() * sizeof(E));
     E *x, *a0, *a1, *y, *yr, *b0, *b1;
     CHECK(hipMalloc(&x, hx.size() * sizeof(E)));
     CHECK(hipMemcpy(x, hx.data(), hx.size() * sizeof(E), hipMemcpyHostToDevice));
@@ -404,11 +424,14 @@ int main(int argc, char **argv) {
             const int outn = L % 2 == 1 ? 2880 : 1920;
             std::vector<E> h2(outn), h1(outn);
             CHECK(hipMemcpy(h2.data(), yr, outn * sizeof(E), hipMemcpyDeviceToHost));
+            write_file("yref_L" + std::to_string(L) + ".bin", h2.data(), outn * sizeof(E));
             size_t diff = 0, missing = 0;
             int timeouts = 0;
             std::string ids;
             for (int k = 0; k < P; ++k) {
                 CHECK(hipMemcpy(h1.data(), py[k], outn * sizeof(E), hipMemcpyDeviceToHost));
+                write_file("ypar" + std::to_string(k) + "_L" + std::to_string(L) + ".bin",
+                           h1.data(), outn * sizeof(E));
                 for (int i = 0; i < outn; ++i) diff += std::memcmp(&h1[i], &h2[i], sizeof(E)) != 0;
                 int herr = 0;
                 CHECK(hipMemcpy(&herr, perr[k], sizeof(int), hipMemcpyDeviceToHost));
@@ -435,6 +458,19 @@ int main(int argc, char **argv) {
             const float t_all = time_us([&] { all(L); }, reps);
             const float t_one = time_us([&] { launch_k(0, L, nullptr); }, reps);
             const float t_batch = time_us([&] { batch(L); }, reps);
+            // the timed runs' barriers too: a stack that gave up waiting ran a layer early
+            int timed_timeouts = 0;
+            for (int k = 0; k < P; ++k) {
+                int herr = 0;
+                CHECK(hipMemcpy(&herr, perr[k], sizeof(int), hipMemcpyDeviceToHost));
+                timed_timeouts += herr;
+            }
+            if (timed_timeouts) {
+                std::printf("{\"form\": \"one_xcd_parallel\", \"stacks\": %d, \"layers\": %d, "
+                            "\"error\": \"a barrier reached its spin bound in a timed run\", "
+                            "\"xcd_ids\": [%s]}\n", P, L, ids.c_str());
+                continue;
+            }
             std::printf("{\"form\": \"one_xcd_parallel\", \"stacks\": %d, \"rank\": %d, \"layers\": %d, "
                         "\"parallel_us\": %.3f, \"one_stack_us\": %.3f, \"batched_per_layer_us\": %.3f, "
                         "\"outputs_differing\": %zu, \"outputs\": %d, \"units_missing\": %zu, "
@@ -482,6 +518,10 @@ int main(int argc, char **argv) {
             std::vector<E> h1(outn), h2(outn);
             CHECK(hipMemcpy(h1.data(), y, outn * sizeof(E), hipMemcpyDeviceToHost));
             CHECK(hipMemcpy(h2.data(), yr, outn * sizeof(E), hipMemcpyDeviceToHost));
+            const std::string tag = std::string(STACK_XCD ? "xcd" : "all") + "_T" +
+                                    std::to_string(T) + "_L" + std::to_string(L);
+            write_file("y_" + tag + (pf ? "_pf1.bin" : "_pf0.bin"), h1.data(), outn * sizeof(E));
+            write_file("yref_" + tag + ".bin", h2.data(), outn * sizeof(E));
             // a differing output still holding the fill pattern was never written
             size_t diff = 0, unwritten = 0;
             int first = -1;

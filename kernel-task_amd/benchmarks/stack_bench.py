@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import os
 import subprocess
 import sys
 from pathlib import Path
@@ -46,7 +47,8 @@ def build(verbose: bool = False) -> list[Path]:
     for form, xcd in FORMS.items():
         cmd = [build_ext._hipcc(), *build_ext.HIPCC_FLAGS, f"-DSTACK_XCD={xcd}", "-DSTACK_RANK=8",
                str(SOURCE), "-o", str(binary(form)), f"-L{lib}", "-l:libtrk.so",
-               f"-Wl,-rpath,{lib}"]
+               # found relative to the binary, so a copy of the tree uses its own library
+               f"-Wl,-rpath,$ORIGIN/{os.path.relpath(lib, BIN)}"]
         if verbose:
             print(" ".join(cmd), flush=True)
         done = subprocess.run(cmd, capture_output=True, text=True)
@@ -57,15 +59,21 @@ def build(verbose: bool = False) -> list[Path]:
 
 
 def run(form: str, tokens: int, layers: list[int], timeout: float = 240.0,
-        parallel: int = 0) -> list[dict]:
+        parallel: int = 0, dump: Path | None = None) -> list[dict]:
     """Run one form (with `parallel` > 0: that many one-XCD stacks side by side); returns its
-    JSON lines. Raises if the program fails or reports an error."""
-    import os
-
+    JSON lines. With `dump`, the program writes x, each layer's cores and every checked
+    output into that directory (raw fp16: x.bin, core_l<l>_k<k>.bin, y_<form>_T<T>_L<L>_pf<p>.bin,
+    yref_<form>_T<T>_L<L>.bin; side by side ypar<k>_L<L>.bin and yref_L<L>.bin). Raises if the
+    program fails or reports an error."""
     path = binary(form)
     if not path.exists():
         raise RuntimeError(f"{path} is not built; run with --build first")
-    env = dict(os.environ, STACK_PAR=str(parallel)) if parallel else None
+    env = dict(os.environ)
+    if parallel:
+        env["STACK_PAR"] = str(parallel)
+    if dump is not None:
+        Path(dump).mkdir(parents=True, exist_ok=True)
+        env["STACK_DUMP"] = str(dump)
     done = subprocess.run([str(path), str(tokens), *map(str, layers)], capture_output=True,
                           text=True, timeout=timeout, env=env)
     rows = [json.loads(ln) for ln in done.stdout.splitlines() if ln.startswith("{")]

@@ -2,13 +2,20 @@
 L alternating 1920->2880 / 2880->1920 rank-8 layers in one launch must give bit for bit the
 output of the same tiles launched once per layer, in both forms (every XCD with device-scope
 barriers; one XCD with L2 barriers, with and without the core-slice prefetch across them),
-with no barrier reaching its spin bound. The binaries are built by __graft_entry__.build()."""
+with no barrier reaching its spin bound. Both, the stack and the per-layer launches, are also
+checked against the float64 oracle chain (oracle.ring_oracle.tr_forward per layer, each layer's
+output rounded to fp16 as the stack stores it) on the x and cores the program wrote, under the
+fp16 rule: so the 2880->1920 layer tile, which no library table holds, is pinned too. The
+binaries are built by __graft_entry__.build()."""
 from __future__ import annotations
 
 import importlib.util
 from pathlib import Path
 
+import numpy as np
 import pytest
+
+from oracle import ring_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -19,11 +26,36 @@ stack_bench = importlib.util.module_from_spec(spec)
 spec.loader.exec_module(stack_bench)
 
 
+UP, DOWN = ((8, 12, 20), (12, 10, 24)), ((12, 10, 24), (8, 12, 20))
+RANK = 8
+
+
+def oracle_chain(dump: Path, tokens: int, layers: int) -> np.ndarray:
+    """The stack's L-layer output by the float64 oracle, layer by layer from the x and cores
+    the program wrote, each layer's output rounded to fp16 as the stack's activations are."""
+    a = np.fromfile(dump / "x.bin", dtype=np.float16).reshape(tokens, 1920)
+    for l in range(layers):
+        ins, outs = UP if l % 2 == 0 else DOWN
+        cores = [np.fromfile(dump / f"core_l{l}_k{k}.bin", dtype=np.float16)
+                 .reshape(RANK, outs[k], ins[k], RANK).astype(np.float64) for k in range(3)]
+        a = ring_oracle.tr_forward(a.astype(np.float64), cores).astype(np.float16)
+    return a.astype(np.float64)
+
+
+def check_against_oracle(got_file: Path, want: np.ndarray) -> float:
+    got = np.fromfile(got_file, dtype=np.float16).astype(np.float64).reshape(want.shape)
+    err = np.abs(got - want)
+    assert np.isfinite(got).all(), got_file.name
+    assert (err <= 0.02 + 0.02 * np.abs(want)).all(), (got_file.name, err.max())
+    assert err.max() <= 1e-2 * np.abs(want).max(), (got_file.name, err.max())
+    return float(err.max())
+
+
 @pytest.mark.parametrize("form", ["all", "xcd"])
 @pytest.mark.parametrize("tokens", [1, 3])
-def test_stack_matches_per_layer_launches(form, tokens):
+def test_stack_matches_per_layer_launches(form, tokens, tmp_path):
     print(f"case: stack form={form} tokens={tokens} layers=2,7", flush=True)
-    rows = stack_bench.run(form, tokens, [2, 7], timeout=120)
+    rows = stack_bench.run(form, tokens, [2, 7], timeout=120, dump=tmp_path)
     assert len(rows) == (2 if form == "all" else 4)
     for r in rows:
         print(r, flush=True)
@@ -37,14 +69,20 @@ def test_stack_matches_per_layer_launches(form, tokens):
         assert r["outputs_differing"] == 0, r
         assert r["barrier_timeouts"] == 0, r
         assert r["outputs"] == (2880 if r["layers"] % 2 else 1920) * tokens
+        L = r["layers"]
+        want = oracle_chain(tmp_path, tokens, L)
+        tag = f"{form}_T{tokens}_L{L}"
+        for name in (f"y_{tag}_pf{int(r['prefetch'])}.bin", f"yref_{tag}.bin"):
+            err = check_against_oracle(tmp_path / name, want)
+            print(f"{name}: max abs error {err:.3e} against the oracle chain", flush=True)
 
 
-def test_stacks_side_by_side_each_on_its_own_xcd():
+def test_stacks_side_by_side_each_on_its_own_xcd(tmp_path):
     """Two one-XCD stacks at once on two streams: each keeps the workgroups on its own XCD
     (XCC_ID), both outputs equal the per-layer launches."""
     print("case: 2 one-XCD stacks side by side, layers=2,7", flush=True)
     try:
-        rows = stack_bench.run("xcd", 1, [2, 7], timeout=120, parallel=2)
+        rows = stack_bench.run("xcd", 1, [2, 7], timeout=120, parallel=2, dump=tmp_path)
     except RuntimeError as e:
         # a stack whose workgroups were not dealt one residue class per XCD ends its
         # barriers at the spin bound and reports it: the form does not apply there
@@ -59,3 +97,7 @@ def test_stacks_side_by_side_each_on_its_own_xcd():
         ids = r["xcd_ids"]
         assert len(ids) == 2 and all(len(x) == 1 for x in ids) and ids[0] != ids[1], r
         assert r["outputs_differing"] == 0 and r["outputs"] == 2 * (2880 if r["layers"] % 2 else 1920), r
+        want = oracle_chain(tmp_path, 1, r["layers"])
+        for name in (f"ypar0_L{r['layers']}.bin", f"ypar1_L{r['layers']}.bin",
+                     f"yref_L{r['layers']}.bin"):
+            check_against_oracle(tmp_path / name, want)
