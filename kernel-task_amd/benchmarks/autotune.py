@@ -15,10 +15,13 @@ count, src/factorized_inference/v3g_tuned.py:4-17). Timing, median of three bloc
 - HIP events around the replay of a HIP graph of back-to-back calls of one tile. This gives
   the GPU time per call without the host's per-call cost (6-8 us through run_variant), which
   would hide the differences between fast tiles;
-- for tiles that take 12 us or more, HIP events around back-to-back eager calls on the
-  stream instead, as bench.py times them. The host cost is hidden behind the kernels there,
-  and graph replays ranked some multi-stage tiles differently from eager calls (Llama up
-  T=128: a graph put two tiles 1 % apart, eager calls 7 % apart the other way).
+- for tiles that take 12 us or more (--eager-from-us; 0 re-times every tile), HIP events
+  around back-to-back eager calls on the stream instead, as bench.py times them: the plan
+  routed to the tile and called through its per-call path, whose host cost (~2.4 us a call)
+  stays hidden behind the kernels. Graph replays ranked some tiles differently from eager
+  calls (Llama up T=128: a graph put two tiles 1 % apart, eager calls 7 % apart the other
+  way; tiles numbered over the whole launch, Tile.YM, won graph replays at 1920->2880 R8
+  T=8-32 and lost eager calls by ~1 us).
 
 Every variant's output is checked against the shape's default variant before it may win (bitwise equality
 is not expected across tiles: the stage-3 summation order differs). Timings within 1 % count
@@ -92,7 +95,7 @@ def eager_us(fn, calls: int, blocks: int = 3) -> float:
     return statistics.median(out)
 
 
-EAGER_FROM_US = 12.0  # tiles this slow (graph-timed) are re-timed with eager calls
+EAGER_FROM_US = 12.0  # tiles this slow (graph-timed) are re-timed with eager calls (--eager-from-us)
 PLACEMENT_TIE = 0.01  # timings this close count as equal: the fewer XCDs win
 
 
@@ -110,7 +113,8 @@ def winner(row: dict[str, float], tiles: dict) -> str:
     return min(close, key=lambda n: (xcds(tiles[n][1]), row[n]))
 
 
-def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
+def tune_shape(shape: tilegen.ShapeDecl, budget_s: float,
+               eager_from_us: float = EAGER_FROM_US) -> tuple[dict, dict]:
     dtype = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[shape.dtype]
     tol = 1e-4 if dtype is torch.float32 else 0.02  # the acceptance rule of the dtype
     spec = TRSpec(shape.ins, shape.outs, shape.rank)
@@ -125,10 +129,11 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
         tiles[names[i]] = key
     measured: dict[int, dict[str, float]] = {}
     t_end = time.perf_counter() + budget_s
+    default = {T: run.plan.select(T) for T in GRID}  # before any routing below
     for T in GRID:
         x = torch.randn(T, spec.in_features, device="cuda", dtype=dtype,
                         generator=torch.Generator(device="cuda").manual_seed(T))
-        ref = run(x).float()
+        ref = run.run_variant(x, default[T]).float()
         scale = ref.abs().max().item()
         row = {}
         for i, v in variants:
@@ -148,10 +153,16 @@ def tune_shape(shape: tilegen.ShapeDecl, budget_s: float) -> tuple[dict, dict]:
             one = (time.perf_counter() - t0) * 1e6
             calls = max(5, min(50, int(2e3 / max(one, 1.0))))
             us = graph_us(fn, calls)
-            if us >= EAGER_FROM_US:
-                for _ in range(calls):  # the clock settles under load first
-                    fn()
-                us = eager_us(fn, calls)
+            if us >= eager_from_us:
+                # the per-call path of bench.py with the plan routed to this tile: its host
+                # cost (~2.4 us a call) stays below the kernels, unlike run_variant's
+                run.plan.set_variant(1, 1 << 30, i)
+                fast = lambda: run(x)  # noqa: E731
+                # blocks of ~20 ms: short blocks of a few-us kernel vary by several percent
+                n = max(calls, min(4000, int(2e4 / max(us, 1.0))))
+                for _ in range(n):  # the clock settles under load first
+                    fast()
+                us = eager_us(fast, n)
             row[names[i]] = us
         measured[T] = row
         best = winner(row, tiles)
@@ -187,6 +198,11 @@ def main() -> int:
     ap.add_argument("--out", type=Path, required=True)
     ap.add_argument("--shapes", default="", help="comma-separated shape keys (default: all)")
     ap.add_argument("--seconds-per-shape", type=float, default=60.0)
+    ap.add_argument("--eager-from-us", type=float, default=EAGER_FROM_US,
+                    help="re-time with eager calls every tile whose graph time reaches this (0: "
+                         "every tile). Graph replays keep the L2 warm across kernels where eager "
+                         "launches do not, which ranked tiles differently on MI355X: one that "
+                         "shares fewer core slices per XCD won graph replays and lost eager calls")
     ap.add_argument("--measurements", type=Path, default=Path("gpurun_out/autotune_us.json"),
                     help="where the raw per-candidate timings go (not part of the tables)")
     args = ap.parse_args()
@@ -209,7 +225,8 @@ def main() -> int:
             if wanted and shape.key not in wanted:
                 continue
             prev = result.get(shape.key) or tilegen.load_tuned().get(shape.key) or {}
-            result[shape.key], raw[shape.key] = tune_shape(shape, args.seconds_per_shape)
+            result[shape.key], raw[shape.key] = tune_shape(shape, args.seconds_per_shape,
+                                                           args.eager_from_us)
             if prev.get("extra"):  # index-only alternatives outlive a retune
                 result[shape.key]["extra"] = prev["extra"]
             for path, data in ((args.out, result), (args.measurements, raw)):

@@ -184,8 +184,8 @@ def kcfg_of(label: str) -> tuple[tuple, tuple] | None:
     if not m:
         return None
     f = [int(v) for v in m.group(1).split(",") if v]
-    f += [0] * (24 - len(f))
-    return tuple(f[1:4]), tuple(f[11:24])
+    f += [0] * (25 - len(f))
+    return tuple(f[1:4]), tuple(f[11:25])
 
 
 def cases(trace: Path, details: dict, max_gap_us: float = 30.0) -> list[dict]:

@@ -158,6 +158,10 @@ struct KCfg {
                              // XL..7 exit at once, so the working ones share XL L2s: each core
                              // slice crosses from HBM at most XL times and a cache line of y is
                              // written back by at most XL L2s (for launches that fit XL x 32 CUs)
+    int YM;                  // workgroup -> (unit, token tile) numbering (unit_of_workgroup):
+                             // 0 = per token tile, 1 = over the whole launch, each XCD taking
+                             // one contiguous range of (token tile, unit), so every unit of a
+                             // token tile, hence every writer of its lines of y, shares an L2
 };
 
 // K orders of the packed second- and last-core sections a variant reads (its chain's layout):
@@ -370,6 +374,7 @@ struct Geo {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
     static_assert(C.XL == 0 || C.XL == 1 || C.XL == 2 || C.XL == 4, "XL is 0, 1, 2 or 4");
     static_assert(C.XL == 0 || NBLK % C.XL == 0, "XL must divide the workgroups of a token tile");
+    static_assert(C.YM == 0 || (C.YM == 1 && C.XL == 0), "YM is 0, or 1 on all 8 XCDs");
     static_assert(C.WIDE >= 0 && C.WIDE <= NW && (C.WIDE == 0 || NW % C.WIDE == 0),
                   "WIDE is 0 or divides the waves");
     static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
@@ -1330,23 +1335,39 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     }
 }
 
-// The work unit (tile index within a token tile) of workgroup column `bx`, or -1 for a
-// workgroup that has no work. Workgroups are dealt round-robin to the 8 XCDs, each with its
-// own L2 (with a multiple of 8 columns, the linear workgroup index has the residue of bx
-// modulo 8). A launch on XL XCDs keeps the workgroups dealt to XCDs 0..XL-1. The units are
-// renumbered so that consecutive ones (the same first-core digit f, hence the same Fs slice)
-// share an XCD.
+// The work unit (tile index within a token tile, .x) and token tile (.y) of workgroup
+// (bx, by), or .x = -1 for a workgroup that has no work. The dispatcher deals workgroups to
+// the 8 XCDs, each with its own L2, round-robin in launch order (x fastest), so workgroup
+// lin = by * NBLK + bx runs on XCD lin % 8. A launch on XL XCDs keeps the workgroups dealt to
+// XCDs 0..XL-1. Otherwise the units are renumbered so that consecutive ones share an XCD:
+//   YM = 0  within each token tile (with NBLK a multiple of 8): consecutive units have the
+//           same first-core digit f, hence the same first-core slice, which each XCD then
+//           fetches for its share of f only;
+//   YM = 1  over the whole launch: XCD x takes the x-th contiguous range of the launch's
+//           (token tile, unit) pairs, ordered token tile first. Every unit of a token tile,
+//           and so every workgroup writing a given line of y, is then on one XCD (at most two
+//           at a range boundary): one L2 writes each line back, where per-token-tile
+//           numbering spreads a line's first-core digits over up to 8 L2s. Each XCD needs the
+//           slices of every f (and only its token tiles' rows of x).
+// Both numberings are bijections of the launch's workgroups onto its (unit, token tile) pairs.
 template <KCfg C>
-__device__ __forceinline__ int unit_of_workgroup(int bx) {
+__device__ __forceinline__ int2 unit_of_workgroup(int bx, int by) {
     using G = Geo<C>;
     if constexpr (C.XL) {
-        if (bx % 8 >= C.XL) return -1;
+        if (bx % 8 >= C.XL) return {-1, by};
         const int w = (bx / 8) * C.XL + bx % 8;  // XCD w % XL, 0 <= w < NBLK
-        return (w % C.XL) * (G::NBLK / C.XL) + w / C.XL;
+        return {(w % C.XL) * (G::NBLK / C.XL) + w / C.XL, by};
+    } else if constexpr (C.YM) {
+        const int n = G::NBLK * int(gridDim.y), lin = by * G::NBLK + bx;
+        const int xcd = lin % 8, base = n / 8, rem = n % 8;
+        // XCD xcd holds workgroups xcd, xcd + 8, ...: base + (xcd < rem) of them, the k-th
+        // taking pair g of the XCD's range, which starts after those of XCDs 0..xcd-1
+        const int g = xcd * base + (xcd < rem ? xcd : rem) + lin / 8;
+        return {g % G::NBLK, g / G::NBLK};
     } else if constexpr (G::NBLK % 8 == 0) {
-        return (bx % 8) * (G::NBLK / 8) + bx / 8;
+        return {(bx % 8) * (G::NBLK / 8) + bx / 8, by};
     }
-    return bx;
+    return {bx, by};
 }
 
 inline const char *xl_tag(int xl) {
@@ -1379,9 +1400,9 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
     __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
 
-    const int b = unit_of_workgroup<C>(blockIdx.x);
-    if (b < 0) return;  // uniform per workgroup, before any barrier or access
-    ring3_unit<C, EPI>(x, Fk, Sk, Lk, y, T, epi_mode, aux, b, blockIdx.y, Fs, Ss, Ls, Xs, Ub, Vb);
+    const int2 u = unit_of_workgroup<C>(blockIdx.x, blockIdx.y);
+    if (u.x < 0) return;  // uniform per workgroup, before any barrier or access
+    ring3_unit<C, EPI>(x, Fk, Sk, Lk, y, T, epi_mode, aux, u.x, u.y, Fs, Ss, Ls, Xs, Ub, Vb);
 }
 
 template <KCfg C>
@@ -1435,15 +1456,15 @@ __global__ void __launch_bounds__(Geo<C>::NT)
     __shared__ __attribute__((aligned(16))) E Xs[G::NBUF * G::szXs];
     __shared__ __attribute__((aligned(16))) E Ub[G::NBUF2 * G::szUb];
     __shared__ __attribute__((aligned(16))) E Vb[G::NBUF2 * G::szVb];
-    const int b = unit_of_workgroup<C>(blockIdx.x);
-    if (b < 0) return;
+    const int2 u = unit_of_workgroup<C>(blockIdx.x, blockIdx.y);
+    if (u.x < 0) return;
     const CoreSections<E> up{reinterpret_cast<const E *>(packed_u + offF),
                              reinterpret_cast<const E *>(packed_u + offS),
                              reinterpret_cast<const E *>(packed_u + offL)};
     ring3_unit<C, true, NoHook, true>(x, reinterpret_cast<const E *>(packed_g + offF),
                                       reinterpret_cast<const E *>(packed_g + offS),
                                       reinterpret_cast<const E *>(packed_g + offL), y, T,
-                                      TRK_EPI_SILU_MUL, nullptr, b, blockIdx.y, Fs, Ss, Ls, Xs,
+                                      TRK_EPI_SILU_MUL, nullptr, u.x, u.y, Fs, Ss, Ls, Xs,
                                       Ub, Vb, NoHook{}, up);
 }
 
@@ -1483,9 +1504,9 @@ struct Shape {
 };
 constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
                     int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0, int S1 = 0,
-                    int XL = 0) {
+                    int XL = 0, int YM = 0) {
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
-                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL};
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL, YM};
 }
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) \
@@ -1527,14 +1548,15 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
             char s1[8] = "";
             if (k.S1) std::snprintf(s1, sizeof(s1), "_s%d", k.S1);
             std::snprintf(v.name, sizeof(v.name),
-                          "ring3_mfma_wide%d%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
+                          "ring3_mfma_wide%d%s%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
                           k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "",
-                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, xl_tag(k.XL), k.F,
+                          k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, xl_tag(k.XL),
+                          k.YM ? "_g" : "", k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         } else {
-            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
                           k.NW == 8 ? "_w8" : "", k.PIPE == 2 ? "_p2" : k.PIPE ? "_p" : "",
-                          xl_tag(k.XL), k.F,
+                          xl_tag(k.XL), k.YM ? "_g" : "", k.F,
                           k.S, k.L, k.TT, k.FC,
                           k.SC, k.LC, k.IC, k.KS3, k.NACC);
         }

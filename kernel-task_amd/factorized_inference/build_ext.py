@@ -144,7 +144,8 @@ def _build_torchcall(verbose: bool) -> None:
            f"-I{root / 'include'}", f"-I{root / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
            f"-I{rocm}/include", f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
            str(CSRC / "trk_torchcall.cpp"), "-o", str(TORCHCALL.with_suffix(".tmp")),
-           f"-L{root / 'lib'}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_python",
+           f"-L{root / 'lib'}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip",
+           "-ltorch_python",
            f"-L{PACKAGE}", "-l:libtrk.so", "-Wl,-rpath,$ORIGIN"]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -99,18 +99,22 @@ class Tile:
     #                stage results, three steps' stages in one barrier interval
     S1: int = 0    # WIDE stage-1 row tiles per wave (0: the kernel's default split)
     XL: int = 0    # XCDs the launch's work runs on: 0 = all 8; 1, 2 or 4 (KCfg::XL)
+    YM: int = 0    # 1: workgroups numbered over the whole launch, one contiguous range of
+    #                (token tile, unit) per XCD (KCfg::YM); 0: within each token tile
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
         a = [self.TT, self.FC, self.SC, self.LC, self.IC, self.KS3, self.NACC]
-        if (self.WIDE, self.MF2, self.NW, self.PIPE, self.XL) != (0, 16, 4, 0, 0):
+        if (self.WIDE, self.MF2, self.NW, self.PIPE, self.XL, self.YM) != (0, 16, 4, 0, 0, 0):
             a += [self.WIDE, self.MF2, self.NW]
-        if self.PIPE or self.S1 or self.XL:
+        if self.PIPE or self.S1 or self.XL or self.YM:
             a.append(self.PIPE)
-        if self.S1 or self.XL:
+        if self.S1 or self.XL or self.YM:
             a.append(self.S1)
-        if self.XL:
+        if self.XL or self.YM:
             a.append(self.XL)
+        if self.YM:
+            a.append(self.YM)
         return ", ".join(map(str, a))
 
 
@@ -350,6 +354,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (t.S1 == 0 or (wide and WM1 > 0 and NW % WM1 == 0), "S1 must split the stage-1 rows"),
         (t.XL in (0, 1, 2, 4), "XL is 0, 1, 2 or 4"),
         (t.XL == 0 or nblk % t.XL == 0, "XL must divide the workgroups of a token tile"),
+        (t.YM == 0 or (t.YM == 1 and t.XL == 0), "YM is 0, or 1 on all 8 XCDs"),
         (c.xrow or c.IN % (16 // eb) == 0, "scatter loader reads x rows in 16-byte vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= N2R * P2 * eb, "stage-3 reduction does not fit in Ub"),
@@ -548,7 +553,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
 
 
 _VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?(?:_s(\d+))?|(_w8)?(_p2?)?)"
-                           r"(_xl|_x[24])?<(\d)(\d)(\d),"
+                           r"(_xl|_x[24])?(_g)?<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -558,13 +563,14 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     if not m:
         raise ValueError(f"not an MFMA variant name: {name!r}")
     wide = int(m.group(1) or 0)
-    order = tuple(int(m.group(i)) for i in (9, 10, 11))
-    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(12, 19))
+    order = tuple(int(m.group(i)) for i in (10, 11, 12))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(13, 20))
     pipe_tag = m.group(4) or m.group(7) or ""
     pipe = 2 if pipe_tag.endswith("2") else 1 if pipe_tag else 0
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
                        8 if (m.group(3) or m.group(6)) else 4, pipe, int(m.group(5) or 0),
-                       {None: 0, "_xl": 1, "_x2": 2, "_x4": 4}[m.group(8)])
+                       {None: 0, "_xl": 1, "_x2": 2, "_x4": 4}[m.group(8)],
+                       1 if m.group(9) else 0)
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:

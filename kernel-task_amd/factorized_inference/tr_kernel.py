@@ -8,11 +8,12 @@ prepare time, a tiling/variant choice per token count) with its own mechanics:
            (jit.py: the generator's table compiled once, cached), at the next power-of-two
            kernel rank when the cores' rank has none (zero-padded ring links, exact);
            trk_pack packs the cores into one device buffer (no dense W, padding only)
-  call     one C++ call per input (_trktorch.forward): check x, allocate the output with
-           torch's caching allocator, trk_forward on the caller's current stream. No
-           workspace, counters or other state survives a call, so one prepared object may
-           be used from several streams. Inputs that need checking or copying go through
-           the Python path below, which raises or copies first.
+  call     one C++ call per input (the call slot of _trktorch.Op, PreparedTRKernel's base):
+           check x, allocate the output with torch's caching allocator, trk_forward on the
+           caller's current stream. No workspace, counters or other state survives a call,
+           so one prepared object may be used from several streams. Inputs that need
+           checking or copying go through the Python path below (_checked_call), which
+           raises or copies first.
 
   epilogues accumulate(x) stores y in fp32; forward_add(x, h) and forward_silu_mul(x, g)
            fuse a residual add or a SwiGLU gate into the kernel's output store
@@ -96,16 +97,26 @@ def make_plan(spec: TRSpec, dtype: torch.dtype) -> _lib.Plan:
     return padded if padded.has_mfma else plan
 
 
+try:  # the base whose C++ call slot runs a prepared operator's calls (built with libtrk.so)
+    from . import _trktorch as _native_call
+    _CallBase = _native_call.Op
+except ImportError:  # not built: PreparedTRKernel() raises in _torch_call()
+    _CallBase = object
+
+
 def current_stream_handle(device_index: int) -> int:
     """hipStream_t of torch's current stream on `device_index`, as an integer."""
     return _raw_stream(device_index)
 
 
-class PreparedTRKernel:
+class PreparedTRKernel(_CallBase):
     """Callable returned by prepare_optimized for cores on a ROCm device.
 
-    fp16, bf16 and fp32 cores are supported; x must have the cores' dtype and device. The
-    output is a new [T, out_features] tensor written on the caller's current stream.
+    fp16, bf16 and fp32 cores are supported; x must have the cores' dtype and device.
+    `run(x)` returns a new [T, out_features] tensor written on the caller's current stream
+    (reference: PreparedTRKernel.__call__, tr_kernel.py:264-319). The call is the C++ slot of
+    the base class _trktorch.Op; x it does not take goes to _checked_call, which raises or
+    copies it first.
     """
 
     def __init__(self, cores: Sequence[torch.Tensor], spec: TRSpec):
@@ -140,9 +151,11 @@ class PreparedTRKernel:
         self._plan_handle = self.plan.handle
         self._packed_ptr = self.packed.data_ptr()
         torch_call = _torch_call()
-        self._bound = torch_call.bind(self._plan_handle, self._packed_ptr, self.in_features,
-                                      self.out_features, _DTYPES[dtype], self.device_index)
+        bind = (self._plan_handle, self._packed_ptr, self.in_features, self.out_features,
+                _DTYPES[dtype], self.device_index)
+        self._bound = torch_call.bind(*bind)   # the epilogue methods' path (forward())
         self._call = torch_call.forward
+        self._bind_native(*bind)               # what a call of the object runs
 
     # ---- queries -------------------------------------------------------------------------
     @property
@@ -169,7 +182,7 @@ class PreparedTRKernel:
                 return True
         return False
 
-    # ---- calls ---------------------------------------------------------------------------
+    # ---- calls (run(x) is the call slot of the base class) ---------------------------------
     def _check(self, x: torch.Tensor) -> torch.Tensor:
         """x as the kernels read it: same dtype/device, [T, in], contiguous, 16-byte aligned."""
         if x.dtype is not self.dtype or x.get_device() != self.device_index:
@@ -182,10 +195,6 @@ class PreparedTRKernel:
         if not x.is_contiguous() or x.data_ptr() & 15:
             x = x.clone(memory_format=torch.contiguous_format)
         return x
-
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        y = self._call(self._bound, x)
-        return y if y is not None else self._checked_call(x)
 
     def accumulate(self, x: torch.Tensor) -> torch.Tensor:
         """y = TR(cores) x in fp32, [T, out_features]: the kernel's accumulator stored without

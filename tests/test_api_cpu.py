@@ -183,6 +183,32 @@ def test_call_bindings_load_and_check_their_arguments():
         _trktorch.forward(bound)
 
 
+def test_call_slot_takes_the_native_path_or_the_checked_one():
+    # _trktorch.Op, the base of PreparedTRKernel: a call with one argument that the C++ path
+    # takes runs there; every other call (unbound object, x it declines, more arguments)
+    # goes to the instance's _checked_call with the same arguments
+    from factorized_inference import _trktorch
+    from factorized_inference.tr_kernel import PreparedTRKernel
+
+    assert issubclass(PreparedTRKernel, _trktorch.Op)
+    assert "__call__" not in vars(PreparedTRKernel)  # the call is the base's C++ slot
+
+    class Probe(_trktorch.Op):
+        def _checked_call(self, *args, **kwargs):
+            return "checked", args, kwargs
+
+    p = Probe()
+    assert p("x") == ("checked", ("x",), {})           # not bound yet
+    plan = _lib.Plan((2, 3, 2), (2, 4, 3), 2, _lib.DTYPE_F16)
+    with pytest.raises(ValueError, match="null plan"):
+        p._bind_native(0, 0, 12, 24, _lib.DTYPE_F16, 0)
+    p._bind_native(plan.handle, 256, 12, 24, _lib.DTYPE_F16, 0)
+    x = torch.zeros(1, 12, dtype=torch.float16)         # on the CPU: the C++ path declines
+    assert p(x)[0] == "checked" and p(x)[1][0] is x
+    assert p(x, 1) == ("checked", (x, 1), {})
+    assert p(x, epilogue=1)[2] == {"epilogue": 1}
+
+
 @pytest.mark.parametrize("ins,outs,R,dtype", [
     ((8, 12, 20), (12, 10, 24), 8, _lib.DTYPE_F16),
     ((8, 12, 20), (12, 10, 24), 16, _lib.DTYPE_F16),

@@ -171,6 +171,7 @@ def test_order_choice_prefers_least_padded_work():
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 3, 1), "KS3"),
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, PIPE=1), "two steps"),
     (HAND[1], tilegen.Tile(1, 1, 5, 12, 4, 1, 2, PIPE=1), "LDS"),  # fits with one buffer
+    (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, XL=4, YM=1), "YM"),
 ])
 def test_planted_tile_mistakes_are_rejected(shape, tile, why):
     assert why in tilegen.geometry(shape, (2, 1, 0), tile)["reject"]
