@@ -288,15 +288,21 @@ int launch_generic(const Plan &plan, const Variant &v, const void *packed, const
     return check_hip(hipGetLastError(), "trk_forward: generic kernel launch");
 }
 
+// The floors launch like the forward kernels: hipLaunchKernel with an argument array.
 int launch_empty(hipStream_t stream) {
-    hipLaunchKernelGGL(ring3_empty_kernel, dim3(1), dim3(64), 0, stream);
-    return check_hip(hipGetLastError(), "trk_empty_launch");
+    return check_hip(hipLaunchKernel(reinterpret_cast<const void *>(&ring3_empty_kernel), dim3(1),
+                                     dim3(64), nullptr, 0, stream),
+                     "trk_empty_launch");
 }
 
 int launch_empty_args(hipStream_t stream) {
-    hipLaunchKernelGGL(ring3_empty_args_kernel, dim3(1), dim3(64), 0, stream, nullptr, nullptr,
-                       nullptr, nullptr, nullptr, 1, 0, nullptr);
-    return check_hip(hipGetLastError(), "trk_empty_launch_args");
+    const void *p = nullptr;
+    void *q = nullptr;
+    int t = 1, mode = 0;
+    void *args[] = {&p, &p, &p, &p, &q, &t, &mode, &p};
+    return check_hip(hipLaunchKernel(reinterpret_cast<const void *>(&ring3_empty_args_kernel),
+                                     dim3(1), dim3(64), args, 0, stream),
+                     "trk_empty_launch_args");
 }
 
 }  // namespace trk
