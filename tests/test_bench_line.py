@@ -39,12 +39,6 @@ def synthetic_case(label, tokens, i):
         "dense_weight_bytes": 117440512, "passed": True, "achieved_GBps": 31.5987654,
         "frac_hbm": 0.0039498765, "achieved_TFLOPs": 12.7654321, "frac_mfma": 0.005106172,
         "reference_flops": 55296000.0, "frac_mfma_reference_flops": 0.0070912345,
-        "kernel_us": 2.876543 + i, "kernel_min_us": 2.7123, "kernel_median_us": 2.8654,
-        "kernel_dispatches": 400,
-        "kernel_time_source": "trk_time_forward: per-dispatch HIP events (hipExtLaunchKernel), "
-                              "back-to-back launches",
-        "kernel_frac_hbm": 0.004287654, "kernel_frac_mfma": 0.005534567,
-        "kernel_frac_mfma_reference_flops": 0.0076876543,
     }
 
 
