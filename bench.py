@@ -490,7 +490,7 @@ def _rounded(v, digits):
 
 def trace_kernel_figure(variant: str) -> dict | None:
     """The headline kernel's mean dispatch duration in the committed rocprofv3 kernel trace
-    (profiles/ring3_kernel_trace.json, written by benchmarks/counters.py grids from a traced
+    (profiles/ring3_kernel_trace.json, written by benchmarks/counters.py cases from a traced
     run of this script), if that trace is of the same variant."""
     path = ROOT / "profiles" / "ring3_kernel_trace.json"
     try:
