@@ -478,7 +478,8 @@ CASE_COLUMNS = [
     ("dense_us", "dense_stream_us", 2), ("frac_hbm", "frac_hbm", 5),
     ("frac_mfma", "frac_mfma", 4), ("frac_mfma_ref_flops", "frac_mfma_reference_flops", 4),
     ("err", "max_abs_err_vs_fp32", 6),
-    ("extra_bytes", "call_extra_bytes", None), ("variant", "variant", None),
+    ("extra_bytes", "call_extra_bytes", None), ("host_us", "ours_host_us", 1),
+    ("variant", "variant", None),
 ]
 
 
@@ -558,6 +559,12 @@ def build_line(steps, warmup, cases, floors, xcd_local, cpu, default_runtime, tr
                    "hip_force_dev_kernarg": os.environ.get("HIP_FORCE_DEV_KERNARG"),
                    "runtime_default": runtime},
         "dense_stream_us": head["dense_stream_us"],
+        "host_us": head["ours_host_us"],
+        # preparation of the headline operator (packing the cores into the plan's layout)
+        "prepare": {"ms": head["prepare_ms"], "packed_bytes": head["packed_bytes"],
+                    "held_bytes": head["prepare_held_bytes"],
+                    "peak_bytes": head["prepare_peak_bytes"],
+                    "dense_weight_bytes": head["dense_weight_bytes"]},
         "roofline": roof,
         "cpu_baseline": cpu_short,
         "xcd_local": xcd,

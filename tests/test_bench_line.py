@@ -93,6 +93,11 @@ def test_line_fits_the_driver_capture_and_carries_the_contract_fields(bench):
     row = dict(zip(cols, line["cases"][4]))
     assert row["case"] == "r16" and row["T"] == 32 and row["extra_bytes"] == 0
     assert row["ours_us"] == pytest.approx(cases[4]["ours_stream_us"], rel=1e-2)
+    assert row["host_us"] == pytest.approx(cases[4]["ours_host_us"], rel=1e-2)
+    # host latency and preparation cost of the headline operator
+    assert line["host_us"] == cases[0]["ours_host_us"]
+    assert line["prepare"]["ms"] == cases[0]["prepare_ms"]
+    assert line["prepare"]["peak_bytes"] == cases[0]["prepare_peak_bytes"]
 
 
 def test_line_sheds_optional_fields_before_exceeding_the_limit(bench):
