@@ -453,10 +453,7 @@ def main() -> int:
         return 1
     default_runtime = None if args.no_runtime_default else runtime_default_figure(
         args.steps, args.warmup)
-    traffic = None
-    traffic_file = ROOT / "profiles" / "traffic_r8_t1.json"
-    if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+    traffic = traffic_figure(cases[0]["variant"])
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
     details = {"cases": cases, "floors": floors, "xcd_local": xcd_local, "cpu_baseline": cpu,
                "runtime_default": default_runtime}
@@ -503,6 +500,20 @@ def trace_kernel_figure(variant: str) -> dict | None:
             return {"mean_us": r["trace_mean_us"], "source": f"rocprofv3 --kernel-trace, "
                     f"{r['trace_dispatches']} dispatches (profiles/ring3_kernel_trace.json)"}
     return None
+
+
+def traffic_figure(variant: str) -> float | None:
+    """HBM bytes per launch of the headline kernel from the committed counter runs
+    (profiles/traffic_r8_t1.json, FETCH_SIZE + WRITE_SIZE), if they are of the same variant;
+    None otherwise (a default that changed since the counters were taken)."""
+    try:
+        data = json.loads((ROOT / "profiles" / "traffic_r8_t1.json").read_text())
+    except (OSError, ValueError):
+        return None
+    if f"({variant}:" not in data.get("workload", ""):
+        log(f"profiles/traffic_r8_t1.json is of another variant than {variant}: no traffic figure")
+        return None
+    return data.get("hbm_bytes_per_launch")
 
 
 def build_line(steps, warmup, cases, floors, xcd_local, cpu, default_runtime, traffic,

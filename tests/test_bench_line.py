@@ -116,3 +116,10 @@ def test_emit_prints_one_line_last(bench, capsys):
     out = capsys.readouterr().out.splitlines()
     assert json.loads(out[-1])["n_gpus"] == 1
     assert out[-1] == out[-1].strip() and len(out) == 2
+
+
+def test_traffic_figure_only_for_the_variant_it_was_measured_on(bench):
+    data = json.loads((ROOT / "profiles" / "traffic_r8_t1.json").read_text())
+    measured = data["workload"].split("(", 1)[1].split(":", 1)[0]
+    assert bench.traffic_figure(measured) == data["hbm_bytes_per_launch"]
+    assert bench.traffic_figure(measured.replace("ring3_mfma", "ring3_mfma_other")) is None
