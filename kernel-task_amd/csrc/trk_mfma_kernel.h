@@ -378,7 +378,8 @@ struct Geo {
     static_assert(C.WIDE >= 0 && C.WIDE <= NW && (C.WIDE == 0 || NW % C.WIDE == 0),
                   "WIDE is 0 or divides the waves");
     static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
-    static_assert(16 % (FC * TT) == 0, "FC * TT must divide 16 (stage-2 store offsets)");
+    static_assert(W32 || 16 % (FC * TT) == 0,
+                  "FC * TT must divide 16 (stage-2 store offsets of 16x16 tiles)");
     static_assert(KS3 >= 1 && NW % KS3 == 0, "KS3 must divide the waves");
     static_assert(NACC >= 1 && (K3 / 32 / KS3) % NACC == 0, "NACC must divide a wave's K steps");
     static_assert(FC <= oF && SC <= oS && LC <= oL && IC <= nL && TT >= 1, "tile too large");
@@ -1062,9 +1063,18 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     auto vb_tile = [&](int mt, int nt) { return vb_row(mt * 16) + vb_col(nt * 16); };
     const int ub_lane = ub_row(4 * lgrp) + ub_col(lrow);
     const int vb_lane = vb_row(4 * lgrp) + vb_col(lrow);
-    // 32x32 stage-2 tiles: rows mt*32 + 8*g + 4*(lane/32) + e, columns nt*32 + lane%32
+    // 32x32 stage-2 tiles: rows mt*32 + 8*g + 4*(lane/32) + e, columns nt*32 + lane%32. With
+    // Q = TT * FC not dividing 32 the column part does not split into tile and lane parts:
+    // (t, f) = n % Q changes with both, and vb_col32 computes it per tile and lane.
     auto vb_tile32 = [&](int mt, int nt) { return vb_row(mt * 32) + vb_col(nt * 32); };
     const int vb_lane32 = vb_row(4 * (lane >> 5)) + vb_col(lane & 31);
+    const int vb_lane32_row = vb_row(4 * (lane >> 5));
+    auto vb_col32 = [&](int mt, int nt) TRK_INLINE {  // tile (mt, nt) plus this lane's offset
+        if constexpr (32 % G::Q == 0)
+            return vb_lane32 + vb_tile32(mt, nt);
+        else
+            return vb_lane32_row + vb_row(mt * 32) + vb_col(nt * 32 + (lane & 31));
+    };
 
 #pragma unroll
     for (int j = 0; j < G::NYW; ++j)
@@ -1114,7 +1124,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
 #pragma unroll
                     for (int g = 0; g < 4; ++g)
                         if (G::M2 % (32 * G::WM2) == 0 || mt * 32 + 8 * g + 4 * (lane >> 5) < G::M2)
-                            put4(vb + vb_lane32 + vb_tile32(mt, nt) + vb_row(8 * g),
+                            put4(vb + vb_col32(mt, nt) + vb_row(8 * g),
                                  f32x4{d[i][4 * g], d[i][4 * g + 1], d[i][4 * g + 2], d[i][4 * g + 3]});
                 }
             };

@@ -342,7 +342,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (NW in (4, 8), "4 or 8 waves"),
         (0 <= t.WIDE <= NW and (t.WIDE == 0 or NW % t.WIDE == 0), "WIDE divides the waves"),
         (t.MF2 == 16 or (t.MF2 == 32 and wide), "MF2 is 16, or 32 with WIDE"),
-        (16 % (t.FC * t.TT) == 0, "FC * TT must divide 16"),
+        (W32 or 16 % (t.FC * t.TT) == 0, "FC * TT must divide 16 (16x16 stage-2 tiles)"),
         (t.KS3 >= 1 and NW % t.KS3 == 0, "KS3 must divide the waves"),
         (k3steps > 0 and k3steps % t.KS3 == 0, "stage-3 K steps must split over KS3"),
         (t.NACC >= 1 and perk % t.NACC == 0, "NACC must divide a wave's K steps"),
@@ -523,6 +523,19 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
                     if not geometry(shape, order, t)["reject"] and t not in out.values():
                         tag = f"f{fc}" if fc > 1 else f"t{tt}"
                         out[f"{fam}_{tag}k{ks3}n{nacc}_ic{ic}"] = t
+            # first-core chunks that no power of two gives (TT * FC not dividing 16; the
+            # 32x32 stage-2 stores then compute their column offsets per lane): 3 of 24
+            # digits makes one token's workgroups 8, so that 32 tokens fill the 256 CUs once
+            # (measured at 1920->2880 R16 T=32: 12.03 -> 11.27 us against the 192
+            # workgroups of 2 tokens x 2 digits)
+            for fc in (f for f in range(3, 9) if nw == 8 and c.oF % f == 0 and 16 % f):
+                for ks3 in (2, 4):
+                    for ic in (base.IC, 2 * base.IC):
+                        if ic > c.nL or c.nL % ic:
+                            continue
+                        t = Tile(1, fc, base.SC, LC, ic, ks3, 1, wide, 32, nw)
+                        if not geometry(shape, order, t)["reject"] and t not in out.values():
+                            out[f"{fam}_f{fc}k{ks3}n1_ic{ic}"] = t
         # the pipelined main loops for every multi-step tile found so far that still fits
         for name, t in list(out.items()):
             if cdiv(c.nL, t.IC) > 1:

@@ -6,9 +6,10 @@
 - The committed generated sources are what the generator writes now.
 - Every declared shape gets MFMA variants whose default token ranges cover every token
   count, in the chain order the generator chose.
-- Planted mistakes in a tile (a rank that is not a power of two, FC*TT not dividing 16, IC
-  not dividing the last core's input mode, LDS over budget, a pipelined tile of one step, a
-  pipelined tile whose doubled slices no longer fit) are rejected.
+- Planted mistakes in a tile (a rank that is not a power of two, FC*TT not dividing 16 on a
+  16x16 stage-2 tile, IC not dividing the last core's input mode, LDS over budget, a
+  pipelined tile of one step, a pipelined tile whose doubled slices no longer fit) are
+  rejected; FC*TT = 3 is accepted on a 32x32 stage-2 tile.
 """
 from __future__ import annotations
 
@@ -175,6 +176,25 @@ def test_order_choice_prefers_least_padded_work():
 ])
 def test_planted_tile_mistakes_are_rejected(shape, tile, why):
     assert why in tilegen.geometry(shape, (2, 1, 0), tile)["reject"]
+
+
+def test_first_core_chunks_beyond_powers_of_two_only_on_32x32_stage2():
+    # TT*FC = 3: the 32x32 stage-2 stores compute their column offsets per lane, so the
+    # register-resident 32x32 tiles take it; the 16x16 stage-2 tiles keep the split offsets
+    # and need TT*FC to divide 16
+    r16 = HAND[1]
+    wide32 = tilegen.Tile(1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1)
+    assert tilegen.geometry(r16, (2, 1, 0), wide32)["reject"] == ""
+    assert tilegen.geometry(r16, (2, 1, 0), wide32)["NBLK"] == 8  # 24 first-core digits / 3
+    lds16 = tilegen.Tile(1, 3, 2, 12, 4, 4, 1)
+    assert "divide 16" in tilegen.geometry(r16, (2, 1, 0), lds16)["reject"]
+    wide16 = tilegen.Tile(1, 3, 10, 12, 2, 4, 1, 8, 16, 8)
+    assert "divide 16" in tilegen.geometry(r16, (2, 1, 0), wide16)["reject"]
+    # the extended search offers the family on the 24-digit first core only
+    names = tilegen.candidates(r16, (2, 1, 0), extended=True)
+    assert any(t.FC == 3 and t.TT == 1 for t in names.values())
+    assert not any(t.FC * t.TT not in (1, 2, 4, 8, 16)
+                   for t in tilegen.candidates(HAND[3], (2, 1, 0), extended=True).values())
 
 
 def test_rule_ranges_cover_everything():
