@@ -528,6 +528,20 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
             # digits makes one token's workgroups 8, so that 32 tokens fill the 256 CUs once
             # (measured at 1920->2880 R16 T=32: 12.03 -> 11.27 us against the 192
             # workgroups of 2 tokens x 2 digits)
+            # one token with the second core's outputs split in two or four, stage 1 recomputed
+            # per chunk: at few tokens the one-token tiles of all second-core digits are too few
+            # workgroups to fill 256 CUs (measured at Llama down T=8: 128 workgroups of 16 digits
+            # 16.1 us, 256 of 8 digits 11.8 us)
+            for part in (2, 4):
+                sc = cdiv(c.oS, part)
+                if nw != 8 or sc >= base.SC:
+                    continue
+                for ic in (base.IC, 2 * base.IC):
+                    if ic > c.nL or c.nL % ic:
+                        continue
+                    t = Tile(1, 1, sc, LC, ic, 2, 1, wide, 32, nw)
+                    if not geometry(shape, order, t)["reject"] and t not in out.values():
+                        out[f"{fam}_sc{sc}k2n1_ic{ic}"] = t
             for fc in (f for f in range(3, 9) if nw == 8 and c.oF % f == 0 and 16 % f):
                 for ks3 in (2, 4):
                     for ic in (base.IC, 2 * base.IC):
