@@ -542,6 +542,16 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
                     t = Tile(1, 1, sc, LC, ic, 2, 1, wide, 32, nw)
                     if not geometry(shape, order, t)["reject"] and t not in out.values():
                         out[f"{fam}_sc{sc}k2n1_ic{ic}"] = t
+            # and both at once: first-core chunks of 2-8 digits with the whole, half or a
+            # quarter of the second core, so that some chunking fills 256 CUs at each token
+            # count (e.g. 1920->2880 R16 T=16: 3 first-core x 5 second-core digits, 256
+            # workgroups)
+            for fc in (f for f in range(2, 9) if nw == 8 and c.oF % f == 0):
+                for part in (1, 2, 4):
+                    sc = cdiv(c.oS, part)
+                    t = Tile(1, fc, sc, LC, base.IC, 2, 1, wide, 32, nw)
+                    if not geometry(shape, order, t)["reject"] and t not in out.values():
+                        out[f"{fam}_f{fc}sc{sc}k2n1_ic{base.IC}"] = t
             for fc in (f for f in range(3, 9) if nw == 8 and c.oF % f == 0 and 16 % f):
                 for ks3 in (2, 4):
                     for ic in (base.IC, 2 * base.IC):
