@@ -197,6 +197,23 @@ def test_first_core_chunks_beyond_powers_of_two_only_on_32x32_stage2():
                    for t in tilegen.candidates(HAND[3], (2, 1, 0), extended=True).values())
 
 
+def test_extended_search_offers_the_chip_filling_one_token_tiles():
+    # one-token register-resident tiles that split the second core in two or four, and ones
+    # that cross first-core chunks of 2-8 digits with those splits: the families the tuned
+    # tables took at Llama down T=3-8, R16 T=3-4, Llama up from 65 tokens and R8 from 129
+    down = tilegen.candidates(HAND[3], (2, 1, 0), extended=True).values()
+    assert {8, 4} <= {t.SC for t in down if t.TT == 1 and t.FC == 1 and t.MF2 == 32}
+    r16 = tilegen.candidates(HAND[1], (2, 1, 0), extended=True).values()
+    assert any(t.TT == 1 and t.FC == 1 and t.SC == 5 and t.MF2 == 32 for t in r16)
+    up = tilegen.candidates(HAND[2], (0, 1, 2), extended=True).values()
+    assert any(t.TT == 1 and t.FC == 8 and t.SC == 28 and t.MF2 == 32 for t in up)
+    r8 = tilegen.candidates(HAND[0], (2, 1, 0), extended=True).values()
+    assert any(t.TT == 1 and t.FC == 8 and t.SC == 10 and t.WIDE == 4 and t.NW == 8 for t in r8)
+    # every offered tile passes the kernel's constraints
+    for shape, order, tiles in ((HAND[3], (2, 1, 0), down), (HAND[1], (2, 1, 0), r16)):
+        assert all(tilegen.geometry(shape, order, t)["reject"] == "" for t in tiles)
+
+
 def test_rule_ranges_cover_everything():
     for names in (["t1_s1", "mid_half", "mid_all", "wide8x32w8"], ["t1_s2", "mid_all"],
                   ["t1_s1"]):
