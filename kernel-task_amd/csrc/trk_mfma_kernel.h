@@ -162,6 +162,11 @@ struct KCfg {
                              // 0 = per token tile, 1 = over the whole launch, each XCD taking
                              // one contiguous range of (token tile, unit), so every unit of a
                              // token tile, hence every writer of its lines of y, shares an L2
+    int SL;                  // WIDE: 1 = each wave reads its second-core slice after the first
+                             // step's slices are committed, so that the first stage 1 runs
+                             // while it arrives; 0 = right after the first-core slice. The
+                             // slice loads fill the CU's vector-memory queue, and a wave
+                             // cannot pass them until its last one is issued
 };
 
 // K orders of the packed second- and last-core sections a variant reads (its chain's layout):
@@ -375,6 +380,7 @@ struct Geo {
     static_assert(C.XL == 0 || C.XL == 1 || C.XL == 2 || C.XL == 4, "XL is 0, 1, 2 or 4");
     static_assert(C.XL == 0 || NBLK % C.XL == 0, "XL must divide the workgroups of a token tile");
     static_assert(C.YM == 0 || (C.YM == 1 && C.XL == 0), "YM is 0, or 1 on all 8 XCDs");
+    static_assert(C.SL == 0 || (C.SL == 1 && C.WIDE), "SL is 0, or 1 with register-resident slices");
     static_assert(C.WIDE >= 0 && C.WIDE <= NW && (C.WIDE == 0 || NW % C.WIDE == 0),
                   "WIDE is 0 or divides the waves");
     static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
@@ -1001,14 +1007,17 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     // the first- and second-core slices stay resident for the whole call
     RegA<O, G::BM1, G::KF> fa;
     std::conditional_t<G::W32, RegA32<O, G::BM2, G::K2>, RegA<O, G::BM2, G::K2>> sa;
-    if constexpr (G::WIDE) {
-        fa.load(Fk + size_t(f0) * R2 * G::KF, wm1 * G::BM1 * 16, FCv * R2, lrow, lgrp);
+    auto load_sa = [&]() TRK_INLINE {
         if constexpr (G::W32 && s_frag(C))
             sa.load_frag(Sk + size_t(s0) * R * G::K2, wm2 * G::BM2 * 32, SCv * R, lane);
         else if constexpr (G::W32)
             sa.load(Sk + size_t(s0) * R * G::K2, wm2 * G::BM2 * 32, SCv * R, lane);
         else
             sa.load(Sk + size_t(s0) * R * G::K2, wm2 * G::BM2 * 16, SCv * R, lrow, lgrp);
+    };
+    if constexpr (G::WIDE) {
+        fa.load(Fk + size_t(f0) * R2 * G::KF, wm1 * G::BM1 * 16, FCv * R2, lrow, lgrp);
+        if constexpr (!C.SL) load_sa();
     } else {
         cF.issue(Fk + size_t(f0) * R2 * G::KF, 0, FCv * R2 * G::KF / VPE);
         cS.issue(Sk + size_t(s0) * R * G::K2, 0, SCv * R * G::K2 / VPE);
@@ -1046,6 +1055,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
         cS.commit(Ss);
     }
     __syncthreads();
+    if constexpr (C.SL) load_sa();  // SL: after the first step's slices are in LDS
 
     // LDS store offsets of the stage-1 (Ub) and stage-2 (Vb) results, split into a part that
     // depends on the tile only and a part that depends on the lane only.
@@ -1528,9 +1538,9 @@ struct Shape {
 };
 constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
                     int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0, int S1 = 0,
-                    int XL = 0, int YM = 0) {
+                    int XL = 0, int YM = 0, int SL = 0) {
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
-                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL, YM};
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL, YM, SL};
 }
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) \
@@ -1572,10 +1582,10 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
             char s1[8] = "";
             if (k.S1) std::snprintf(s1, sizeof(s1), "_s%d", k.S1);
             std::snprintf(v.name, sizeof(v.name),
-                          "ring3_mfma_wide%d%s%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
+                          "ring3_mfma_wide%d%s%s%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
                           k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "",
                           k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, xl_tag(k.XL),
-                          k.YM ? "_g" : "", k.F,
+                          k.YM ? "_g" : "", k.SL ? "_sl" : "", k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         } else {
             std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",

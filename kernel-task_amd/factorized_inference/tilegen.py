@@ -23,7 +23,8 @@ eighth second-core tiles, single-token tiles without the stage-3 wave reduction,
 last-core inputs per step, a 4-row-group register-resident family on 8 waves, one token
 (and one token with two first-core digits) per register-resident workgroup, the two
 pipelined main loops (PIPE 1 and 2) of every multi-step tile, single-token tiles placed on
-1, 2 or 4 XCDs, larger stage-1 row groups (S1) of the previous winners, and the neighbours
+1, 2 or 4 XCDs, larger stage-1 row groups (S1) of the previous winners, the previous
+register-resident winners with their second-core slice read late (SL), and the neighbours
 of the previous register-resident winners (tokens, first-core digits, main loop, S1 and
 stage-3 split varied together).
 
@@ -101,20 +102,25 @@ class Tile:
     XL: int = 0    # XCDs the launch's work runs on: 0 = all 8; 1, 2 or 4 (KCfg::XL)
     YM: int = 0    # 1: workgroups numbered over the whole launch, one contiguous range of
     #                (token tile, unit) per XCD (KCfg::YM); 0: within each token tile
+    SL: int = 0    # 1: the second-core slice is read after the first step's slices are
+    #                committed, while the first stage 1 runs (KCfg::SL; WIDE only)
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
         a = [self.TT, self.FC, self.SC, self.LC, self.IC, self.KS3, self.NACC]
-        if (self.WIDE, self.MF2, self.NW, self.PIPE, self.XL, self.YM) != (0, 16, 4, 0, 0, 0):
+        if (self.WIDE, self.MF2, self.NW, self.PIPE, self.XL, self.YM, self.SL) != (
+                0, 16, 4, 0, 0, 0, 0):
             a += [self.WIDE, self.MF2, self.NW]
-        if self.PIPE or self.S1 or self.XL or self.YM:
+        if self.PIPE or self.S1 or self.XL or self.YM or self.SL:
             a.append(self.PIPE)
-        if self.S1 or self.XL or self.YM:
+        if self.S1 or self.XL or self.YM or self.SL:
             a.append(self.S1)
-        if self.XL or self.YM:
+        if self.XL or self.YM or self.SL:
             a.append(self.XL)
-        if self.YM:
+        if self.YM or self.SL:
             a.append(self.YM)
+        if self.SL:
+            a.append(self.SL)
         return ", ".join(map(str, a))
 
 
@@ -355,6 +361,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (t.XL in (0, 1, 2, 4), "XL is 0, 1, 2 or 4"),
         (t.XL == 0 or nblk % t.XL == 0, "XL must divide the workgroups of a token tile"),
         (t.YM == 0 or (t.YM == 1 and t.XL == 0), "YM is 0, or 1 on all 8 XCDs"),
+        (t.SL == 0 or (t.SL == 1 and wide), "SL is 0, or 1 with register-resident slices"),
         (c.xrow or c.IN % (16 // eb) == 0, "scatter loader reads x rows in 16-byte vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= N2R * P2 * eb, "stage-3 reduction does not fit in Ub"),
@@ -590,7 +597,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
 
 
 _VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?(?:_s(\d+))?|(_w8)?(_p2?)?)"
-                           r"(_xl|_x[24])?(_g)?<(\d)(\d)(\d),"
+                           r"(_xl|_x[24])?(_g)?(_sl)?<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -600,14 +607,14 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     if not m:
         raise ValueError(f"not an MFMA variant name: {name!r}")
     wide = int(m.group(1) or 0)
-    order = tuple(int(m.group(i)) for i in (10, 11, 12))
-    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(13, 20))
+    order = tuple(int(m.group(i)) for i in (11, 12, 13))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(14, 21))
     pipe_tag = m.group(4) or m.group(7) or ""
     pipe = 2 if pipe_tag.endswith("2") else 1 if pipe_tag else 0
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
                        8 if (m.group(3) or m.group(6)) else 4, pipe, int(m.group(5) or 0),
                        {None: 0, "_xl": 1, "_x2": 2, "_x4": 4}[m.group(8)],
-                       1 if m.group(9) else 0)
+                       1 if m.group(9) else 0, 1 if m.group(10) else 0)
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
@@ -723,8 +730,9 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
     ranges = rule_ranges([n for n, (o, _) in cands.items() if o == first])
     if all_candidates and shape.key in tuned:
         # the previous winners stay candidates, so a new search never loses a tile it had;
-        # an extended search also tries their larger stage-1 row groups and, for the
-        # register-resident winners of 5 tokens or more, their neighbours (a local refinement)
+        # an extended search also tries their larger stage-1 row groups, the register-resident
+        # ones with their second-core slice read late (SL) and, for the register-resident
+        # winners of 5 tokens or more, their neighbours (a local refinement)
         entry = tuned[shape.key]
         for r in entry["ranges"] + entry.get("extra", []):
             order = tuple(r.get("order", entry["order"]))
@@ -740,6 +748,9 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
             if extended:
                 found += [(base + suffix + tag, v)
                           for suffix, v in s1_variants(shape, order, tile).items()]
+                late = replace(tile, SL=1)
+                if tile.WIDE and not tile.SL and not geometry(shape, order, late)["reject"]:
+                    found.append((base + "_sl" + tag, late))
                 if r.get("t_min", 0) >= 5:
                     found += [(base[:40] + suffix + tag, v)
                               for suffix, v in neighbours(shape, order, tile).items()]

@@ -13,6 +13,8 @@
 """
 from __future__ import annotations
 
+from dataclasses import replace
+
 import numpy as np
 import pytest
 
@@ -54,6 +56,10 @@ def test_variant_names_parse_back_to_their_tiles():
         1, 1, 2, 12, 8, 4, 1, XL=4)
     assert parse("ring3_mfma_p_x2<210,1,1,5,12,8,1,2>")[1] == tilegen.Tile(
         1, 1, 5, 12, 8, 1, 2, PIPE=1, XL=2)
+    assert parse("ring3_mfma_wide4x32_sl<210,1,1,10,12,4,2,1>")[1] == tilegen.Tile(
+        1, 1, 10, 12, 4, 2, 1, 4, 32, 4, SL=1)
+    assert parse("ring3_mfma_wide8x32w8p_s4_g_sl<210,1,2,16,16,2,2,1>")[1] == tilegen.Tile(
+        1, 2, 16, 16, 2, 2, 1, 8, 32, 8, 1, 4, YM=1, SL=1)
     with pytest.raises(ValueError):
         parse("ring3_generic<012,rc=8>")
 
@@ -64,6 +70,9 @@ def test_xcd_placed_tiles_emit_every_trailing_argument():
     assert tilegen.Tile(1, 1, 10, 12, 8, 4, 1, 0, 16, 8, XL=1).args() == \
         "1, 1, 10, 12, 8, 4, 1, 0, 16, 8, 0, 0, 1"
     assert tilegen.Tile(1, 1, 2, 12, 8, 4, 1).args() == "1, 1, 2, 12, 8, 4, 1"
+    # so does a tile whose second-core slice is read late (SL, the last argument)
+    assert tilegen.Tile(1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1, SL=1).args() == \
+        "1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1, 0, 0, 0, 1"
     # the headline shape's table carries an XCD-local tile, index-only, beside its winners
     shape = tilegen.BASELINE[0]
     xl = [(n, t, lo, hi) for n, _, t, lo, hi in tilegen.table(shape) if t.XL == 1]
@@ -173,6 +182,7 @@ def test_order_choice_prefers_least_padded_work():
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, PIPE=1), "two steps"),
     (HAND[1], tilegen.Tile(1, 1, 5, 12, 4, 1, 2, PIPE=1), "LDS"),  # fits with one buffer
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, XL=4, YM=1), "YM"),
+    (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, SL=1), "SL"),  # LDS-staged slices
 ])
 def test_planted_tile_mistakes_are_rejected(shape, tile, why):
     assert why in tilegen.geometry(shape, (2, 1, 0), tile)["reject"]
@@ -212,6 +222,19 @@ def test_extended_search_offers_the_chip_filling_one_token_tiles():
     # every offered tile passes the kernel's constraints
     for shape, order, tiles in ((HAND[3], (2, 1, 0), down), (HAND[1], (2, 1, 0), r16)):
         assert all(tilegen.geometry(shape, order, t)["reject"] == "" for t in tiles)
+
+
+def test_extended_search_offers_the_winners_with_the_late_second_core_slice():
+    # every register-resident winner of a tuned table comes back with SL=1 (and the same tile
+    # otherwise); LDS-staged winners do not
+    tuned = tilegen.load_tuned()
+    for shape in tilegen.BASELINE:
+        rows = tilegen.table(shape, tuned, all_candidates=True, extended=True)
+        late = {(o, t) for _, o, t, _, _ in rows if t.SL}
+        for r in tuned[shape.key]["ranges"]:
+            t = tilegen.Tile(**r["tile"])
+            order = tuple(r.get("order", tuned[shape.key]["order"]))
+            assert ((order, replace(t, SL=1)) in late) == bool(t.WIDE), (shape.name, r["name"])
 
 
 def test_rule_ranges_cover_everything():
