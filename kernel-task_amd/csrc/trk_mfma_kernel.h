@@ -778,6 +778,7 @@ struct NoHook {
 // calls it. The standalone kernel below calls it once per workgroup; a persistent caller may
 // call it for several units and layers, with a barrier (__syncthreads) between units.
 // hook, when given, is called by every thread once the unit's core-slice loads are in flight
+// (with SL, the second-core slice's come after the first commit, past the hook)
 // and before any load of x, which is then issued after it: a persistent caller's wait for the
 // layer that writes x (the core slices do not depend on it). Without a hook the loads keep
 // the standalone order. COHERENT_X reads x with device-scope loads, which the CU's L1 does not
