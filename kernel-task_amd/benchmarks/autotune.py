@@ -3,10 +3,10 @@ declared shape over a grid of token counts and write the fastest per token range
 
     python -m factorized_inference.tilegen --all   # compile every candidate (from kernel-task_amd/)
     python -m factorized_inference.build_ext
-    python kernel-task_amd/benchmarks/autotune.py --out gpurun_out/tuned.json    # on an MI355X
-        (the winners' table; the raw timings of every candidate go to --measurements,
-        gpurun_out/autotune_us.json by default, and never into the tree)
-    cp gpurun_out/tuned.json kernel-task_amd/csrc/gen/tuned.json
+    python kernel-task_amd/benchmarks/autotune.py --out OUT/tuned.json    # on an MI355X
+        (the winners' table; the raw timings of every candidate go to --measurements, a file
+        outside the source tree, and never into the tables)
+    cp OUT/tuned.json kernel-task_amd/csrc/gen/tuned.json
     python -m factorized_inference.tilegen && python -m factorized_inference.build_ext
 
 Role of the reference's tools/qwen_sweep.py and tools/gen_v3g_tuned.py (a sweep of V3G

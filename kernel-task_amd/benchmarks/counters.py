@@ -12,7 +12,7 @@ kernel traces.
     # row also gives the longest back-to-back block of that kernel and grid
     python kernel-task_amd/benchmarks/counters.py grids TRACE.csv [--out FILE.json]
     # one row per bench.py case: its kernel's durations in a traced bench.py run, beside the
-    # case's stream time from that run's details file (gpurun_out/bench_details.json)
+    # case's stream time from that run's details file (bench.py's DETAILS)
     python kernel-task_amd/benchmarks/counters.py cases TRACE.csv DETAILS.json [--out FILE]
 
 A probe run (bench.py --traffic-probe CALLS) launches one tensor-ring kernel CALLS times and
