@@ -162,11 +162,13 @@ struct KCfg {
                              // 0 = per token tile, 1 = over the whole launch, each XCD taking
                              // one contiguous range of (token tile, unit), so every unit of a
                              // token tile, hence every writer of its lines of y, shares an L2
-    int SL;                  // WIDE: 1 = each wave reads its second-core slice after the first
-                             // step's slices are committed, so that the first stage 1 runs
-                             // while it arrives; 0 = right after the first-core slice. The
-                             // slice loads fill the CU's vector-memory queue, and a wave
-                             // cannot pass them until its last one is issued
+    int SL;                  // 1: the second-core slice arrives while the first stage 1 runs.
+                             // WIDE: each wave reads it after the first step's slices are
+                             // committed (the slice loads fill the CU's vector-memory queue,
+                             // and a wave cannot pass them until its last one is issued);
+                             // LDS-staged: it is read with the other slices but written to
+                             // LDS after the first stage 1. 0: read, and written, with the
+                             // first-core slice
 };
 
 // K orders of the packed second- and last-core sections a variant reads (its chain's layout):
@@ -380,7 +382,7 @@ struct Geo {
     static_assert(C.XL == 0 || C.XL == 1 || C.XL == 2 || C.XL == 4, "XL is 0, 1, 2 or 4");
     static_assert(C.XL == 0 || NBLK % C.XL == 0, "XL must divide the workgroups of a token tile");
     static_assert(C.YM == 0 || (C.YM == 1 && C.XL == 0), "YM is 0, or 1 on all 8 XCDs");
-    static_assert(C.SL == 0 || (C.SL == 1 && C.WIDE), "SL is 0, or 1 with register-resident slices");
+    static_assert(C.SL == 0 || C.SL == 1, "SL is 0 or 1");
     static_assert(C.WIDE >= 0 && C.WIDE <= NW && (C.WIDE == 0 || NW % C.WIDE == 0),
                   "WIDE is 0 or divides the waves");
     static_assert(C.MF2 == 16 || (C.MF2 == 32 && WIDE), "MF2 is 16, or 32 with WIDE");
@@ -1053,7 +1055,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
     commit_step(0, 0);
     if constexpr (!G::WIDE) {
         cF.commit(Fs);
-        cS.commit(Ss);
+        if constexpr (!C.SL) cS.commit(Ss);
     }
     __syncthreads();
     if constexpr (C.SL) load_sa();  // SL: after the first step's slices are in LDS
@@ -1208,6 +1210,11 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
         }
     };
 
+    // SL on LDS-staged tiles: the second-core slice, loaded in the prologue, goes to LDS after
+    // the first stage 1, which does not read it (stage 2 does, after the next barrier)
+    auto late_s = [&]() TRK_INLINE {
+        if constexpr (!G::WIDE && C.SL) cS.commit(Ss);
+    };
     if constexpr (C.PIPE == 1) {
         // Two buffers of Ls and Xs. Step k+1's slices are committed while step k's are still
         // being read, and stage 3 of step k runs in the same barrier interval as stage 1 of
@@ -1220,6 +1227,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
         // second barrier of step k-1.
         issue_step(G::IC);
         stage1(Xs, Ub);
+        late_s();
         __syncthreads();
         stage2(Ub, Vb);
         for (int step = 0; step < G::NSTEP; ++step) {
@@ -1262,6 +1270,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
                 if (s1) stage1(xs_i, ub_i);
                 if (s2) stage2(ub_p, vb_p);
             }
+            if (i == 0) late_s();  // before the barrier that opens the first stage 2
         }
     } else {
         for (int step = 0; step < G::NSTEP; ++step) {
@@ -1275,6 +1284,7 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
             // this step computes, so a step pays no memory latency of its own
             if (step + 1 < G::NSTEP) issue_step(iL0 + G::IC);
             stage1(Xs, Ub);
+            if (step == 0) late_s();
             __syncthreads();
             stage2(Ub, Vb);
             __syncthreads();
@@ -1589,9 +1599,9 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
                           k.YM ? "_g" : "", k.SL ? "_sl" : "", k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         } else {
-            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
+            std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",
                           k.NW == 8 ? "_w8" : "", k.PIPE == 2 ? "_p2" : k.PIPE ? "_p" : "",
-                          xl_tag(k.XL), k.YM ? "_g" : "", k.F,
+                          xl_tag(k.XL), k.YM ? "_g" : "", k.SL ? "_sl" : "", k.F,
                           k.S, k.L, k.TT, k.FC,
                           k.SC, k.LC, k.IC, k.KS3, k.NACC);
         }

@@ -24,7 +24,7 @@ last-core inputs per step, a 4-row-group register-resident family on 8 waves, on
 (and one token with two first-core digits) per register-resident workgroup, the two
 pipelined main loops (PIPE 1 and 2) of every multi-step tile, single-token tiles placed on
 1, 2 or 4 XCDs, larger stage-1 row groups (S1) of the previous winners, the previous
-register-resident winners with their second-core slice read late (SL), and the neighbours
+winners with their second-core slice arriving during the first stage 1 (SL), and the neighbours
 of the previous register-resident winners (tokens, first-core digits, main loop, S1 and
 stage-3 split varied together).
 
@@ -102,8 +102,9 @@ class Tile:
     XL: int = 0    # XCDs the launch's work runs on: 0 = all 8; 1, 2 or 4 (KCfg::XL)
     YM: int = 0    # 1: workgroups numbered over the whole launch, one contiguous range of
     #                (token tile, unit) per XCD (KCfg::YM); 0: within each token tile
-    SL: int = 0    # 1: the second-core slice is read after the first step's slices are
-    #                committed, while the first stage 1 runs (KCfg::SL; WIDE only)
+    SL: int = 0    # 1: the second-core slice arrives while the first stage 1 runs: read after
+    #                the first commit (register-resident) or written to LDS after the first
+    #                stage 1 (LDS-staged) (KCfg::SL)
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
@@ -361,7 +362,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (t.XL in (0, 1, 2, 4), "XL is 0, 1, 2 or 4"),
         (t.XL == 0 or nblk % t.XL == 0, "XL must divide the workgroups of a token tile"),
         (t.YM == 0 or (t.YM == 1 and t.XL == 0), "YM is 0, or 1 on all 8 XCDs"),
-        (t.SL == 0 or (t.SL == 1 and wide), "SL is 0, or 1 with register-resident slices"),
+        (t.SL in (0, 1), "SL is 0 or 1"),
         (c.xrow or c.IN % (16 // eb) == 0, "scatter loader reads x rows in 16-byte vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= N2R * P2 * eb, "stage-3 reduction does not fit in Ub"),
@@ -730,9 +731,9 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
     ranges = rule_ranges([n for n, (o, _) in cands.items() if o == first])
     if all_candidates and shape.key in tuned:
         # the previous winners stay candidates, so a new search never loses a tile it had;
-        # an extended search also tries their larger stage-1 row groups, the register-resident
-        # ones with their second-core slice read late (SL) and, for the register-resident
-        # winners of 5 tokens or more, their neighbours (a local refinement)
+        # an extended search also tries their larger stage-1 row groups, each of them with its
+        # second-core slice arriving during the first stage 1 (SL) and, for the
+        # register-resident winners of 5 tokens or more, their neighbours (a local refinement)
         entry = tuned[shape.key]
         for r in entry["ranges"] + entry.get("extra", []):
             order = tuple(r.get("order", entry["order"]))
@@ -749,7 +750,7 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
                 found += [(base + suffix + tag, v)
                           for suffix, v in s1_variants(shape, order, tile).items()]
                 late = replace(tile, SL=1)
-                if tile.WIDE and not tile.SL and not geometry(shape, order, late)["reject"]:
+                if not tile.SL and not geometry(shape, order, late)["reject"]:
                     found.append((base + "_sl" + tag, late))
                 if r.get("t_min", 0) >= 5:
                     found += [(base[:40] + suffix + tag, v)
