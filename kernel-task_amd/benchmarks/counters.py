@@ -178,14 +178,14 @@ def grids(trace: Path, max_gap_us: float = 30.0) -> list[dict]:
 
 
 def kcfg_of(label: str) -> tuple[tuple, tuple] | None:
-    """(chain order, tile fields TT..SL) of a 'ring3<KCfg fields>' label; fields the
+    """(chain order, tile fields TT..TP) of a 'ring3<KCfg fields>' label; fields the
     compiler's name leaves out at the end are zero."""
     m = re.fullmatch(r"ring3<([-0-9,]*)>", label)
     if not m:
         return None
     f = [int(v) for v in m.group(1).split(",") if v]
-    f += [0] * (26 - len(f))
-    return tuple(f[1:4]), tuple(f[11:26])
+    f += [0] * (27 - len(f))
+    return tuple(f[1:4]), tuple(f[11:27])
 
 
 def cases(trace: Path, details: dict, max_gap_us: float = 30.0) -> list[dict]:

@@ -169,6 +169,10 @@ struct KCfg {
                              // LDS-staged: it is read with the other slices but written to
                              // LDS after the first stage 1. 0: read, and written, with the
                              // first-core slice
+    int TP;                  // pair-and-tail stage 2 (Geo::TAIL): 1 = the tail waves, which run
+                             // one MFMA per K step, hold the SIMDs' issue priority while they
+                             // run it (s_setprio), so that they finish before the waves with
+                             // whole row tiles instead of after them, waiting on LDS alone
 };
 
 // K orders of the packed second- and last-core sections a variant reads (its chain's layout):
@@ -331,6 +335,7 @@ struct Geo {
     static constexpr bool TAIL = W32 && WN2 == 1 && BM2 == 1 && NW == 8 && TAILR > 0 &&
                                  M2T32 < NW && (NW / 2) % TAILR == 0;
     static constexpr int TAILJ = TAIL ? (NW / 2) / TAILR : 1;
+    static_assert(C.TP == 0 || (C.TP == 1 && TAIL), "TP needs the pair-and-tail stage 2");
     static constexpr int NBUF = C.PIPE ? 2 : 1;  // buffers of the per-step slices
     static constexpr int NBUF2 = C.PIPE == 2 ? 2 : 1;  // buffers of the stage results
     // LDS row pitches for the fragment shape each buffer is read with (Ub by 32x32x16 MFMAs in
@@ -1152,10 +1157,13 @@ __device__ __forceinline__ void ring3_unit(const typename Ops<C.dt>::E *__restri
                 }
             };
             if constexpr (G::TAIL) {
-                if (wave < HW)
+                if (wave < HW) {
                     reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, 1>(sa, ub, 0, lane, st);
-                else
+                } else {
+                    if constexpr (C.TP) __builtin_amdgcn_s_setprio(1);
                     reg_gemm32<O, 1, G::K2, G::P2, G::N2T32, G::TAILJ>(sa, ub, wn2, lane, st);
+                    if constexpr (C.TP) __builtin_amdgcn_s_setprio(0);
+                }
             } else if (G::M2T32 % G::WM2 == 0 || wm2 * G::BM2 < G::M2T32) {  // else no rows
                 reg_gemm32<O, G::BM2, G::K2, G::P2, G::N2T32, G::WN2>(sa, ub, wn2, lane, st);
             }
@@ -1549,9 +1557,9 @@ struct Shape {
 };
 constexpr KCfg tile(Shape s, int TT, int FC, int SC, int LC, int IC, int KS3, int NACC,
                     int WIDE = 0, int MF2 = 16, int NW = 4, int PIPE = 0, int S1 = 0,
-                    int XL = 0, int YM = 0, int SL = 0) {
+                    int XL = 0, int YM = 0, int SL = 0, int TP = 0) {
     return KCfg{s.dt, s.F, s.S, s.L, s.i0, s.i1, s.i2, s.o0, s.o1, s.o2, s.R,
-                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL, YM, SL};
+                TT, FC, SC, LC, IC, KS3, NACC, WIDE, MF2, NW, PIPE, S1, XL, YM, SL, TP};
 }
 
 #define TRK_ENTRY(CFG, TMIN, TMAX) \
@@ -1593,10 +1601,10 @@ inline int register_entries(Plan *plan, const Entry *entries, int count) {
             char s1[8] = "";
             if (k.S1) std::snprintf(s1, sizeof(s1), "_s%d", k.S1);
             std::snprintf(v.name, sizeof(v.name),
-                          "ring3_mfma_wide%d%s%s%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
+                          "ring3_mfma_wide%d%s%s%s%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>", k.WIDE,
                           k.MF2 == 32 ? "x32" : "", k.NW == 8 ? "w8" : "",
                           k.PIPE == 2 ? "p2" : k.PIPE ? "p" : "", s1, xl_tag(k.XL),
-                          k.YM ? "_g" : "", k.SL ? "_sl" : "", k.F,
+                          k.YM ? "_g" : "", k.SL ? "_sl" : "", k.TP ? "_tp" : "", k.F,
                           k.S, k.L, k.TT, k.FC, k.SC, k.LC, k.IC, k.KS3, k.NACC);
         } else {
             std::snprintf(v.name, sizeof(v.name), "ring3_mfma%s%s%s%s%s<%d%d%d,%d,%d,%d,%d,%d,%d,%d>",

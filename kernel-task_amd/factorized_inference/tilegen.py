@@ -24,7 +24,8 @@ last-core inputs per step, a 4-row-group register-resident family on 8 waves, on
 (and one token with two first-core digits) per register-resident workgroup, the two
 pipelined main loops (PIPE 1 and 2) of every multi-step tile, single-token tiles placed on
 1, 2 or 4 XCDs, larger stage-1 row groups (S1) of the previous winners, the previous
-winners with their second-core slice arriving during the first stage 1 (SL), and the neighbours
+winners with their second-core slice arriving during the first stage 1 (SL) and with the
+issue priority of their stage-2 tail waves (TP, where they have some), and the neighbours
 of the previous register-resident winners (tokens, first-core digits, main loop, S1 and
 stage-3 split varied together).
 
@@ -105,23 +106,18 @@ class Tile:
     SL: int = 0    # 1: the second-core slice arrives while the first stage 1 runs: read after
     #                the first commit (register-resident) or written to LDS after the first
     #                stage 1 (LDS-staged) (KCfg::SL)
+    TP: int = 0    # 1: the tail waves of a pair-and-tail stage 2 hold the issue priority while
+    #                they run it (KCfg::TP; tiles with tail waves only)
 
     def args(self) -> str:
         """Arguments of tile(shape, ...) in the variant tables."""
         a = [self.TT, self.FC, self.SC, self.LC, self.IC, self.KS3, self.NACC]
-        if (self.WIDE, self.MF2, self.NW, self.PIPE, self.XL, self.YM, self.SL) != (
-                0, 16, 4, 0, 0, 0, 0):
+        # each optional argument is spelled out when it or any later one differs from its default
+        tail = [self.PIPE, self.S1, self.XL, self.YM, self.SL, self.TP]
+        last = max((i for i, v in enumerate(tail) if v), default=-1)
+        if last >= 0 or (self.WIDE, self.MF2, self.NW) != (0, 16, 4):
             a += [self.WIDE, self.MF2, self.NW]
-        if self.PIPE or self.S1 or self.XL or self.YM or self.SL:
-            a.append(self.PIPE)
-        if self.S1 or self.XL or self.YM or self.SL:
-            a.append(self.S1)
-        if self.XL or self.YM or self.SL:
-            a.append(self.XL)
-        if self.YM or self.SL:
-            a.append(self.YM)
-        if self.SL:
-            a.append(self.SL)
+        a += tail[:last + 1]
         return ", ".join(map(str, a))
 
 
@@ -313,6 +309,10 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
     else:
         BM1, WM1 = cdiv(M1T, NW), NW
     BM2 = cdiv(M2T32 if W32 else M2T, WM2)
+    # the pair-and-tail stage 2 (Geo::TAIL): waves 4-7 split the row tiles past the first 4
+    tailr = M2T32 - NW // 2
+    g["TAIL"] = (W32 and NW // WM2 == 1 and BM2 == 1 and NW == 8 and tailr > 0 and M2T32 < NW
+                 and (NW // 2) % tailr == 0)
     sz = {
         "Fs": 8 if wide else M1 * PF,
         "Ss": 8 if wide else M2P * P2,
@@ -363,6 +363,7 @@ def geometry(shape: ShapeDecl, order: tuple, t: Tile) -> dict:
         (t.XL == 0 or nblk % t.XL == 0, "XL must divide the workgroups of a token tile"),
         (t.YM == 0 or (t.YM == 1 and t.XL == 0), "YM is 0, or 1 on all 8 XCDs"),
         (t.SL in (0, 1), "SL is 0 or 1"),
+        (t.TP == 0 or (t.TP == 1 and g["TAIL"]), "TP needs the pair-and-tail stage 2"),
         (c.xrow or c.IN % (16 // eb) == 0, "scatter loader reads x rows in 16-byte vectors"),
         (lds <= LDS_LIMIT, f"LDS {lds} B exceeds 160 KB"),
         (red_floats * 4 <= N2R * P2 * eb, "stage-3 reduction does not fit in Ub"),
@@ -598,7 +599,7 @@ def candidates(shape: ShapeDecl, order: tuple | None = None,
 
 
 _VARIANT_NAME = re.compile(r"ring3_mfma(?:_wide(\d)(x32)?(w8)?(p2?)?(?:_s(\d+))?|(_w8)?(_p2?)?)"
-                           r"(_xl|_x[24])?(_g)?(_sl)?<(\d)(\d)(\d),"
+                           r"(_xl|_x[24])?(_g)?(_sl)?(_tp)?<(\d)(\d)(\d),"
                            r"(\d+),(\d+),(\d+),(\d+),(\d+),(\d+),(\d+)>")
 
 
@@ -608,14 +609,15 @@ def parse_variant_name(name: str) -> tuple[tuple, Tile]:
     if not m:
         raise ValueError(f"not an MFMA variant name: {name!r}")
     wide = int(m.group(1) or 0)
-    order = tuple(int(m.group(i)) for i in (11, 12, 13))
-    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(14, 21))
+    order = tuple(int(m.group(i)) for i in (12, 13, 14))
+    TT, FC, SC, LC, IC, KS3, NACC = (int(m.group(i)) for i in range(15, 22))
     pipe_tag = m.group(4) or m.group(7) or ""
     pipe = 2 if pipe_tag.endswith("2") else 1 if pipe_tag else 0
     return order, Tile(TT, FC, SC, LC, IC, KS3, NACC, wide, 32 if m.group(2) else 16,
                        8 if (m.group(3) or m.group(6)) else 4, pipe, int(m.group(5) or 0),
                        {None: 0, "_xl": 1, "_x2": 2, "_x4": 4}[m.group(8)],
-                       1 if m.group(9) else 0, 1 if m.group(10) else 0)
+                       1 if m.group(9) else 0, 1 if m.group(10) else 0,
+                       1 if m.group(11) else 0)
 
 
 def rule_ranges(names: list[str]) -> dict[str, tuple[int, int]]:
@@ -732,8 +734,9 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
     if all_candidates and shape.key in tuned:
         # the previous winners stay candidates, so a new search never loses a tile it had;
         # an extended search also tries their larger stage-1 row groups, each of them with its
-        # second-core slice arriving during the first stage 1 (SL) and, for the
-        # register-resident winners of 5 tokens or more, their neighbours (a local refinement)
+        # second-core slice arriving during the first stage 1 (SL), those with tail waves in
+        # stage 2 with the tail waves' issue priority (TP) and, for the register-resident
+        # winners of 5 tokens or more, their neighbours (a local refinement)
         entry = tuned[shape.key]
         for r in entry["ranges"] + entry.get("extra", []):
             order = tuple(r.get("order", entry["order"]))
@@ -752,6 +755,9 @@ def table(shape: ShapeDecl, tuned: dict | None = None, all_candidates: bool = Fa
                 late = replace(tile, SL=1)
                 if not tile.SL and not geometry(shape, order, late)["reject"]:
                     found.append((base + "_sl" + tag, late))
+                prio = replace(tile, TP=1)
+                if not tile.TP and not geometry(shape, order, prio)["reject"]:
+                    found.append((base + "_tp" + tag, prio))
                 if r.get("t_min", 0) >= 5:
                     found += [(base[:40] + suffix + tag, v)
                               for suffix, v in neighbours(shape, order, tile).items()]

@@ -139,4 +139,4 @@ def test_cases_match_each_bench_case_to_its_kernel_and_grid(tmp_path):
     assert head["stream_us"] == 3.1
     assert "trace_mean_us" not in other and other["stream_us"] == 5.0
     assert counters.kcfg_of(counters.kernel_label(RING)) == (
-        (2, 1, 0), (1, 1, 2, 12, 8, 4, 1, 0, 16, 4, 0, 0, 0, 0, 0))
+        (2, 1, 0), (1, 1, 2, 12, 8, 4, 1, 0, 16, 4, 0, 0, 0, 0, 0, 0))

@@ -62,6 +62,8 @@ def test_variant_names_parse_back_to_their_tiles():
         1, 2, 16, 16, 2, 2, 1, 8, 32, 8, 1, 4, YM=1, SL=1)
     assert parse("ring3_mfma_x4_sl<210,1,1,2,12,8,4,1>")[1] == tilegen.Tile(
         1, 1, 2, 12, 8, 4, 1, XL=4, SL=1)
+    assert parse("ring3_mfma_wide8x32w8p_sl_tp<210,1,3,10,12,2,4,1>")[1] == tilegen.Tile(
+        1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1, SL=1, TP=1)
     with pytest.raises(ValueError):
         parse("ring3_generic<012,rc=8>")
 
@@ -72,9 +74,12 @@ def test_xcd_placed_tiles_emit_every_trailing_argument():
     assert tilegen.Tile(1, 1, 10, 12, 8, 4, 1, 0, 16, 8, XL=1).args() == \
         "1, 1, 10, 12, 8, 4, 1, 0, 16, 8, 0, 0, 1"
     assert tilegen.Tile(1, 1, 2, 12, 8, 4, 1).args() == "1, 1, 2, 12, 8, 4, 1"
-    # so does a tile whose second-core slice is read late (SL, the last argument)
+    # so do a tile whose second-core slice is read late (SL) and one with tail priority (TP,
+    # the last argument)
     assert tilegen.Tile(1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1, SL=1).args() == \
         "1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1, 0, 0, 0, 1"
+    assert tilegen.Tile(1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1, TP=1).args() == \
+        "1, 3, 10, 12, 2, 4, 1, 8, 32, 8, 1, 0, 0, 0, 0, 1"
     # the headline shape's table carries an XCD-local tile, index-only, beside its winners
     shape = tilegen.BASELINE[0]
     xl = [(n, t, lo, hi) for n, _, t, lo, hi in tilegen.table(shape) if t.XL == 1]
@@ -197,6 +202,8 @@ def test_order_choice_prefers_least_padded_work():
     (HAND[1], tilegen.Tile(1, 1, 5, 12, 4, 1, 2, PIPE=1), "LDS"),  # fits with one buffer
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, XL=4, YM=1), "YM"),
     (HAND[0], tilegen.Tile(1, 1, 2, 12, 8, 4, 1, SL=2), "SL"),
+    # tail priority on a tile whose stage 2 has no tail waves (8 row tiles on 8 waves)
+    (HAND[3], tilegen.Tile(1, 2, 16, 16, 2, 2, 1, 8, 32, 8, 1, 4, TP=1), "TP"),
 ])
 def test_planted_tile_mistakes_are_rejected(shape, tile, why):
     assert why in tilegen.geometry(shape, (2, 1, 0), tile)["reject"]
@@ -238,17 +245,21 @@ def test_extended_search_offers_the_chip_filling_one_token_tiles():
         assert all(tilegen.geometry(shape, order, t)["reject"] == "" for t in tiles)
 
 
-def test_extended_search_offers_the_winners_with_the_late_second_core_slice():
+def test_extended_search_offers_the_winners_with_late_slices_and_tail_priority():
     # every winner of a tuned table comes back with SL=1 and the same tile otherwise, the
     # register-resident and the LDS-staged ones alike
     tuned = tilegen.load_tuned()
     for shape in tilegen.BASELINE:
         rows = tilegen.table(shape, tuned, all_candidates=True, extended=True)
         late = {(o, t) for _, o, t, _, _ in rows if t.SL}
+        prio = {(o, t) for _, o, t, _, _ in rows if t.TP}
         for r in tuned[shape.key]["ranges"]:
             t = tilegen.Tile(**r["tile"])
             order = tuple(r.get("order", tuned[shape.key]["order"]))
             assert t.SL or (order, replace(t, SL=1)) in late, (shape.name, r["name"])
+            # and those whose stage 2 has tail waves also with the tail waves' priority
+            tail = tilegen.geometry(shape, order, t)["TAIL"]
+            assert t.TP or ((order, replace(t, TP=1)) in prio) == tail, (shape.name, r["name"])
 
 
 def test_rule_ranges_cover_everything():
