@@ -528,7 +528,8 @@ def build_line(steps, warmup, cases, floors, xcd_local, cpu, default_runtime, tr
             "frac": achieved / peak_hbm_gbs, "traffic": traffic,
             "kernel": head["variant"], "algorithmic_bytes": head["bytes"],
             "time_us": head["ours_stream_us"],
-            "time_source": "HIP events over the timed block, divided by its launches",
+            "time_source": "HIP events (hipEventDisableSystemFence) over the timed block, "
+                           "divided by its launches",
             "mfma_frac": head["frac_mfma"],
             "mfma_frac_reference_flops": head["frac_mfma_reference_flops"],
             "floor_stream_empty_args_us": floors.get("stream_empty_launch_args_us"),
