@@ -146,7 +146,10 @@ class PreparedTRKernel(_CallBase):
             _lib.check(_lib.load().trk_pack(self.plan.handle, g[0].data_ptr(), g[1].data_ptr(),
                                             g[2].data_ptr(), self.packed.data_ptr(),
                                             current_stream_handle(self.device_index)))
-            del g  # packing is stream-ordered before any later call on this stream
+            # the packed cores are complete before prepare returns, so a first call on any
+            # stream (not only the one that packed) reads them whole
+            torch.cuda.current_stream(self.device_index).synchronize()
+            del g
         self._forward, self._forward_variant, self._forward_epilogue = _fast_forward()
         self._plan_handle = self.plan.handle
         self._packed_ptr = self.packed.data_ptr()

@@ -181,6 +181,22 @@ def test_non_contiguous_input_and_side_stream():
     check_result(y, expected, torch.float16)
 
 
+def test_first_call_on_a_stream_that_never_waited_for_the_packing():
+    """prepare_optimized returns with the packed cores complete, so a first call on a stream
+    that never waited for the packing stream reads them whole."""
+    spec = TRSpec(rank=16)
+    cores = make_cores(spec, device="cuda", dtype=torch.float16, seed=6)
+    x = gpu_x(spec, 4, 14, torch.float16)
+    expected = oracle_y(x, cores, spec)
+    torch.cuda.synchronize()  # the cores and x are ready; nothing waits for the packing below
+    run = prepare_optimized(cores, spec)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        y = run(x)
+    stream.synchronize()
+    check_result(y, expected, torch.float16)
+
+
 def test_one_object_on_concurrent_streams_and_threads():
     """No state survives a call, so one prepared object serves several streams and host threads
     at once (the reference's design B must not: tr_kernel.py:185-187). Results are bitwise
